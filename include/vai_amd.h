@@ -1,0 +1,181 @@
+/*
+ * vai_amd.h -- C ABI of the MI355X (gfx950) kernels behind vAi's matmul hot path.
+ *
+ * Plain pointers and sizes only. Every buffer is device memory the caller owns
+ * (hipMalloc'd, or any device-visible pointer); every launch is asynchronous on
+ * the given stream and returns a vai_status (0 = success). Nothing throws
+ * across this boundary. The library keeps no per-call state besides an
+ * immutable kernel table.
+ *
+ * Callers: the C++ nodes in vai_amd/engine (Linear::run, Convolution::run,
+ * AttentionScores::run, GatedMul::run), which replace the reference's
+ * pipelinePool().request(...) + descriptor write + dispatch sequence.
+ */
+#ifndef VAI_AMD_H
+#define VAI_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* vai_stream_t;   /* == hipStream_t */
+
+/* Status codes. Values >= 1000 are the library's own argument checks; other
+ * non-zero values are hipError_t codes passed through. */
+typedef enum {
+    VAI_OK = 0,
+    VAI_ERR_INVALID_ARG = 1001,    /* null pointer, zero size, bad enum */
+    VAI_ERR_SHAPE = 1002,          /* shapes that do not fit together */
+    VAI_ERR_DTYPE = 1003,          /* a dtype combination the reference rejects */
+    VAI_ERR_WORKSPACE = 1004,      /* workspace missing or too small */
+    VAI_ERR_UNSUPPORTED = 1005,    /* valid, but not implemented here */
+} vai_status;
+
+/* Dtype codes: the reference's DTYPE_F32 / DTYPE_F16 / DTYPE_NONE
+ * (/root/reference/vai/shaders/common/spec_constants.h:6-8). */
+enum { VAI_DTYPE_F32 = 0, VAI_DTYPE_F16 = 1, VAI_DTYPE_NONE = 2 };
+
+/* Epilogue codes in the order of vai::Epilogue
+ * (/root/reference/vai/nodes/common.h:31-39). */
+enum { VAI_EPI_NONE = 0, VAI_EPI_RELU, VAI_EPI_GELU, VAI_EPI_GELU_TANH, VAI_EPI_SILU, VAI_EPI_SIGMOID };
+
+/* vai::ResidualOrder (/root/reference/vai/nodes/common.h:42-45). */
+enum { VAI_RESIDUAL_AFTER_EPILOGUE = 0, VAI_RESIDUAL_BEFORE_EPILOGUE = 1 };
+
+/* ---------------------------------------------------------------------------
+ * Linear: O = s * epi(I . W^T + bias) + R        (residual_order AFTER)
+ *         O = s * epi(I . W^T + bias + R)        (residual_order BEFORE)
+ * I [M,K] (i_dtype), W [N,K] (w_dtype), O [M,N] (o_dtype), bias (b_dtype),
+ * residual R (o_dtype). bias_repeat / residual_repeat: 0 when the operand
+ * covers [M,N], else its element count, read modulo (a [N] row that repeats).
+ * M <= 8 runs the HBM-streaming GEMV (fp32 math on the operands as stored,
+ * the linear-slab contract); M > 8 runs the MFMA GEMM (fp16 staging unless I
+ * and W are both fp32, then fp32 MFMA -- the linear-tile contract).
+ * split_size > 0 forces split-K with K spans of that length (>= 32);
+ * 0 lets the library choose. Split-K needs a workspace of
+ * vai_linear_workspace_size() bytes.
+ *
+ * gated != 0 fuses the reference's GatedMul after this Linear
+ * (/root/reference/vai/nodes/gated-mul.h:9-20): W holds [2H, K] rows (the
+ * activated half first), O is [M, H] with
+ *   O[m,j] = gate_epilogue(Y[m,j]) * Y[m,H+j],  Y = I . W^T + bias,
+ * and epilogue must be NONE, scalar_scale 1, no residual.
+ *
+ * Replaces Linear::prepare/run's dispatches (/root/reference/vai/nodes/
+ * linear.h:2291-2798): linear-slab, linear-tile / linear-cm, linear-reduce.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    void* out;
+    const void* in;
+    const void* weight;
+    const void* bias;        /* NULL: no bias (Linear::hasBias() false) */
+    const void* residual;    /* NULL: no residual */
+    void* workspace;         /* split-K partials; may be NULL when not needed */
+    size_t workspace_bytes;
+    uint32_t M, N, K;        /* N = outDim (= 2H when gated) */
+    int32_t o_dtype, i_dtype, w_dtype, b_dtype;
+    uint32_t epilogue;
+    uint32_t residual_order;
+    uint32_t bias_repeat;
+    uint32_t residual_repeat;
+    float scalar_scale;
+    uint32_t split_size;
+    uint32_t gated;
+    uint32_t gate_epilogue;
+} vai_linear_args;
+
+vai_status vai_linear_launch(const vai_linear_args* args, vai_stream_t stream);
+size_t vai_linear_workspace_size(const vai_linear_args* args);
+
+/* Which kernel vai_linear_launch picks for args (for tests and reports):
+ * writes a short name ("slab", "slab_scalar", "tile_f16_128x128", ...). */
+vai_status vai_linear_plan(const vai_linear_args* args, char* name, size_t name_len, uint32_t* split_count);
+
+/* GatedMul alone: O[r,j] = epi(I[r,j]) * I[r,H+j], I [rows, 2H].
+ * Replaces gated-mul.comp (/root/reference/vai/nodes/gated-mul.h:75-114). */
+vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int32_t i_dtype,
+                                uint32_t rows, uint32_t H, uint32_t epilogue, vai_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Convolution (implicit GEMM): same-padded odd kernel, NCHW.
+ *   out[b,co,ho,wo] = epi(scale[co] * sum_{c,kh,kw} W[co,c,kh,kw] X[b,c,ho*s+kh-p,wo*s+kw-p]
+ *                         + bias[co] (+R)) (+R),   p = kernel/2, Ho = (Hi-1)/s+1.
+ * bias / scale carry w_dtype and may be NULL; residual carries i_dtype.
+ * fp16 weights stage both operands as fp16 (fp16 MFMA); fp32 weights stage
+ * fp32 (fp32 MFMA). fp16 input needs fp16 weights; fp16 output needs fp16
+ * weights (Convolution::validateInputs, /root/reference/vai/nodes/
+ * convolution.h:4137-4160). Replaces runK3S1Implicit / the implicit-GEMM
+ * plan (/root/reference/vai/nodes/convolution.h:6237-6283, 6616-6644).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    void* out;
+    const void* in;
+    const void* weight;
+    const void* bias;
+    const void* scale;
+    const void* residual;
+    uint32_t batch, ci, hi, wi, co, kernel, stride;
+    int32_t o_dtype, i_dtype, w_dtype;
+    uint32_t epilogue;
+    uint32_t residual_order;
+} vai_conv2d_args;
+
+vai_status vai_conv2d_launch(const vai_conv2d_args* args, vai_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Attention scores: S[b,h,i,j] = scale * sum_d Q[b,h,i,d] K[b,h/g,j,d],
+ * g = Hq/Hkv, fp32 accumulation, S fp32. causal != 0 hides key j from query i
+ * when j > i + (Tkv - Tq) (queries align with the keys' end); span > 0 also
+ * hides j < i + Tkv - Tq + 1 - span. Hidden entries are -inf.
+ * Q [batch,Hq,Tq,D], K [batch,Hkv,Tkv,D], same dtype (f16 or f32).
+ * The Q.K^T stage of the reference's attention kernels
+ * (/root/reference/vai/shaders/attention.comp:155-182,
+ *  attention-fa.comp:581-591, common/causal_mask.h:25-42).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    float* scores;
+    const void* q;
+    const void* k;
+    uint32_t batch, hq, hkv, tq, tkv, head_dim;
+    int32_t dtype;
+    float scale;
+    uint32_t causal;
+    uint32_t span;
+} vai_attn_scores_args;
+
+vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Device memory and streams: what the host side (vai::Tensor's pooled
+ * buffers, the reference's eva::Buffer role) and the tests use.
+ * ------------------------------------------------------------------------- */
+vai_status vai_device_count(int* count);
+vai_status vai_set_device(int device);
+vai_status vai_malloc(void** ptr, size_t bytes);
+vai_status vai_free(void* ptr);
+vai_status vai_memcpy_h2d(void* dst, const void* src, size_t bytes, vai_stream_t stream);
+vai_status vai_memcpy_d2h(void* dst, const void* src, size_t bytes, vai_stream_t stream);
+vai_status vai_memcpy_d2d(void* dst, const void* src, size_t bytes, vai_stream_t stream);
+vai_status vai_memset(void* dst, int value, size_t bytes, vai_stream_t stream);
+vai_status vai_stream_create(vai_stream_t* stream);
+vai_status vai_stream_destroy(vai_stream_t stream);
+vai_status vai_stream_sync(vai_stream_t stream);
+vai_status vai_device_sync(void);
+const char* vai_status_string(vai_status status);
+
+/* Timing: launches fn-equivalent work is the caller's; these wrap hipEvents
+ * recorded on the stream the kernels run on. */
+typedef struct ihipEvent_t* vai_event_t;
+vai_status vai_event_create(vai_event_t* ev);
+vai_status vai_event_destroy(vai_event_t ev);
+vai_status vai_event_record(vai_event_t ev, vai_stream_t stream);
+vai_status vai_event_sync(vai_event_t ev);
+vai_status vai_event_elapsed_ms(float* ms, vai_event_t start, vai_event_t stop);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VAI_AMD_H */

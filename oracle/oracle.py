@@ -1,0 +1,169 @@
+"""ctypes front end of the C restatement in vai_oracle.c (test infrastructure).
+
+Every entry point mirrors one reference kernel's numeric contract; see the
+docstrings of vai_oracle.c for the reference file:line each follows.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libvai_oracle.so")
+_lib = None
+
+F32, F16 = 0, 1
+EPILOGUES = {"NONE": 0, "RELU": 1, "GELU": 2, "GELU_TANH": 3, "SILU": 4, "SIGMOID": 5}
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _lib.orc_epilogue.restype = ctypes.c_float
+        _lib.orc_epilogue.argtypes = [ctypes.c_float, ctypes.c_int]
+        _lib.orc_f2h.restype = ctypes.c_uint16
+        _lib.orc_h2f.restype = ctypes.c_float
+        _lib.orc_num_threads.restype = ctypes.c_int
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _dt(a):
+    if a is None:
+        return F32
+    if a.dtype == np.float16:
+        return F16
+    assert a.dtype == np.float32, a.dtype
+    return F32
+
+
+def _c(a):
+    return None if a is None else np.ascontiguousarray(a)
+
+
+# ---- fp16 conversion (reference tensor.cpp:42-90) ---------------------------
+
+def to_f16(x):
+    """fp32 -> fp16 bits as the reference host does it: RNE, subnormals flush."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16(_p(x), _p(out), ctypes.c_size_t(x.size))
+    return out.view(np.float16)
+
+
+def from_f16(h):
+    h = np.ascontiguousarray(h).view(np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().orc_f16_to_f32(_p(h), _p(out), ctypes.c_size_t(h.size))
+    return out
+
+
+def epilogue(x, epi):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_epilogue_vec(_p(x), _p(y), ctypes.c_size_t(x.size), ctypes.c_int(EPILOGUES[epi]))
+    return y
+
+
+# ---- Linear -----------------------------------------------------------------
+
+def linear(inp, weight, bias=None, residual=None, *, epi="NONE", order=0, scale=1.0,
+           out_dtype=np.float32, stage="auto", split_size=0):
+    """O = s*epi(I W^T + b) (+R). stage 'slab' (M <= 8) or 'tile' or 'auto'."""
+    inp, weight, bias, residual = _c(inp), _c(weight), _c(bias), _c(residual)
+    K = weight.shape[-1]
+    N = weight.shape[0]
+    M = inp.size // K
+    if stage == "auto":
+        stage = "slab" if M <= 8 else "tile"
+    out = np.empty(inp.shape[:-1] + (N,), dtype=out_dtype)
+    bias_rep = 0 if bias is None or bias.size == M * N else bias.size
+    res_rep = 0 if residual is None or residual.size == M * N else residual.size
+    lib().orc_linear(_p(out), _dt(out), _p(inp), _dt(inp), _p(weight), _dt(weight),
+                     _p(bias), _dt(bias), ctypes.c_uint32(bias_rep),
+                     _p(residual), ctypes.c_uint32(res_rep),
+                     ctypes.c_uint32(M), ctypes.c_uint32(N), ctypes.c_uint32(K),
+                     ctypes.c_int(EPILOGUES[epi]), ctypes.c_int(order), ctypes.c_float(scale),
+                     ctypes.c_int(1 if stage == "tile" else 0), ctypes.c_uint32(split_size))
+    return out
+
+
+def gemm_f32(a, b):
+    """Plain fp32 O = A B^T (CPU baseline kernel)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    M, K = a.shape
+    N = b.shape[0]
+    out = np.empty((M, N), dtype=np.float32)
+    lib().orc_gemm_f32(_p(out), _p(a), _p(b), ctypes.c_uint32(M), ctypes.c_uint32(N), ctypes.c_uint32(K))
+    return out
+
+
+def linear_reduce(partials, bias=None, residual=None, *, epi="NONE", order=0, scale=1.0):
+    partials = _c(partials)
+    split, MN = partials.shape[0], partials[0].size
+    out = np.empty(partials.shape[1:], dtype=partials.dtype)
+    bias_rep = 0 if bias is None or bias.size == MN else bias.size
+    res_rep = 0 if residual is None or residual.size == MN else residual.size
+    bias, residual = _c(bias), _c(residual)
+    lib().orc_linear_reduce(_p(out), _p(partials), _dt(partials), ctypes.c_uint32(split), ctypes.c_uint32(MN),
+                            _p(bias), _dt(bias), ctypes.c_uint32(bias_rep), _p(residual), ctypes.c_uint32(res_rep),
+                            ctypes.c_int(EPILOGUES[epi]), ctypes.c_int(order), ctypes.c_float(scale))
+    return out
+
+
+def gated_mul(inp, *, epi="SILU", out_dtype=np.float32):
+    inp = _c(inp)
+    H = inp.shape[-1] // 2
+    rows = inp.size // (2 * H)
+    out = np.empty(inp.shape[:-1] + (H,), dtype=out_dtype)
+    lib().orc_gated_mul(_p(out), _dt(out), _p(inp), _dt(inp), ctypes.c_uint32(rows), ctypes.c_uint32(H),
+                        ctypes.c_int(EPILOGUES[epi]))
+    return out
+
+
+def conv2d(x, weight, bias=None, scale=None, residual=None, *, stride=1, epi="NONE", order=0,
+           out_dtype=np.float32):
+    """Same-padded odd-kernel conv, x [..., Ci, Hi, Wi], weight [Co, Ci, k, k]."""
+    x, weight, bias, scale, residual = _c(x), _c(weight), _c(bias), _c(scale), _c(residual)
+    Co, Ci, ks, _ = weight.shape
+    Hi, Wi = x.shape[-2:]
+    batch = x.size // (Ci * Hi * Wi)
+    Ho, Wo = (Hi - 1) // stride + 1, (Wi - 1) // stride + 1
+    out = np.empty(x.shape[:-3] + (Co, Ho, Wo), dtype=out_dtype)
+    lib().orc_conv2d(_p(out), _dt(out), _p(x), _dt(x), _p(weight), _dt(weight), _p(bias), _p(scale), _p(residual),
+                     ctypes.c_uint32(batch), ctypes.c_uint32(Ci), ctypes.c_uint32(Hi), ctypes.c_uint32(Wi),
+                     ctypes.c_uint32(Co), ctypes.c_uint32(ks), ctypes.c_uint32(stride),
+                     ctypes.c_int(EPILOGUES[epi]), ctypes.c_int(order))
+    return out
+
+
+def attn_scores(q, k, *, scale=None, causal=True, span=0):
+    """S = scale * Q K^T per head, -inf where the causal mask hides a key."""
+    q, k = _c(q), _c(k)
+    assert q.dtype == k.dtype
+    Hq, Tq, D = q.shape[-3:]
+    Hkv, Tkv, _ = k.shape[-3:]
+    lead = q.size // (Hq * Tq * D)
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    out = np.empty(q.shape[:-1] + (Tkv,), dtype=np.float32)
+    lib().orc_attn_scores(_p(out), _p(q), _p(k), _dt(q), ctypes.c_uint32(Hq * lead), ctypes.c_uint32(Hkv * lead),
+                          ctypes.c_uint32(Tq), ctypes.c_uint32(Tkv), ctypes.c_uint32(D),
+                          ctypes.c_float(scale), ctypes.c_int(1 if causal else 0), ctypes.c_uint32(span))
+    return out
+
+
+def num_threads():
+    return lib().orc_num_threads()

@@ -1,0 +1,54 @@
+"""Shared test helpers: the reference's draw convention and tolerance tiers.
+
+Tolerance tiers are the reference's (/root/reference/python/tests/
+node_check.py:20-28): (rtol, atol) for numpy.testing.assert_allclose.
+"""
+import numpy as np
+
+from oracle import oracle
+
+EXACT = (0.0, 0.0)
+FP32 = (1e-5, 1e-5)
+TRANS = (1e-4, 1e-5)
+FP16 = (1e-3, 5e-3)
+# BASELINE's fp16-with-fp32-accumulation bound, as an allclose tier.
+FP16_BASELINE = (1e-2, 1e-2)
+
+
+def normal(shape, scale=1.0):
+    return lambda rng: scale * rng.standard_normal(shape)
+
+
+def uniform(shape, low, high):
+    return lambda rng: rng.uniform(low, high, shape)
+
+
+def draw(gen, rng, dtype=np.float32):
+    """Draw as float32 (node_check._draw), then round to fp16 the way the
+    reference host does (tensor.cpp floatToHalf) when dtype is fp16."""
+    a = gen(rng) if callable(gen) else rng.standard_normal(gen)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if np.dtype(dtype) == np.float16:
+        return oracle.to_f16(a)
+    return a
+
+
+def max_rel_err(got, want):
+    """BASELINE's metric: max |got-ref| / max(|ref|, 1e-6 * max|ref|) over finite refs."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    fin = np.isfinite(want)
+    if not fin.any():
+        return 0.0
+    floor = 1e-6 * np.abs(want[fin]).max()
+    return float((np.abs(got[fin] - want[fin]) / np.maximum(np.abs(want[fin]), floor)).max())
+
+
+def assert_close(got, want, tol, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    same_inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), same_inf), f"{what}: -inf pattern differs"
+    assert (got[same_inf] == want[same_inf]).all(), f"{what}: inf sign differs"
+    np.testing.assert_allclose(got[~same_inf], want[~same_inf], rtol=tol[0], atol=tol[1], err_msg=what)

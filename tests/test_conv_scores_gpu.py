@@ -1,0 +1,118 @@
+"""Convolution (implicit GEMM) and attention scores through the C ABI on the
+MI355X vs the oracle.
+
+Conv cases follow /root/reference/python/tests/nodes/test_convolution.py:
+12-87 (k1s1, k3s1 at 12^2 and 28^2, k3s2, k5s1, scale, residual), plus
+BASELINE config 5. Scores: BASELINE config 4 plus GQA, Tq != Tkv and the
+sliding-window span of common/causal_mask.h.
+"""
+import numpy as np
+import pytest
+
+from helpers import FP16, FP32, TRANS, assert_close, draw, normal, uniform
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def run_conv(capi, x, w, b=None, s=None, r=None, out_dtype=np.float32, **kw):
+    d = capi.DeviceArray.from_numpy
+    dx, dw = d(x), d(w)
+    db = d(b) if b is not None else None
+    ds = d(s) if s is not None else None
+    dr = d(r) if r is not None else None
+    Co, _, ks, _ = w.shape
+    stride = kw.get("stride", 1)
+    Hi, Wi = x.shape[-2:]
+    out = capi.DeviceArray(x.shape[:-3] + (Co, (Hi - 1) // stride + 1, (Wi - 1) // stride + 1), out_dtype)
+    capi.conv2d(out, dx, dw, db, ds, dr, **kw)
+    return out.numpy()
+
+
+@pytest.mark.parametrize("ci, co, ks, stride, hw, batch, epi, dt", [
+    (16, 32, 1, 1, 12, 1, "NONE", np.float32),
+    (8, 16, 3, 1, 12, 1, "RELU", np.float32),
+    (8, 16, 3, 1, 28, 2, "SILU", np.float32),
+    (8, 16, 3, 2, 13, 1, "NONE", np.float32),
+    (4, 8, 5, 1, 11, 1, "GELU", np.float32),
+    (32, 64, 3, 1, 20, 1, "SILU", np.float16),
+    (24, 40, 3, 2, 17, 3, "SIGMOID", np.float16),
+    (3, 16, 7, 2, 23, 1, "RELU", np.float16),
+])
+def test_conv(gpu, ci, co, ks, stride, hw, batch, epi, dt):
+    rng = np.random.default_rng(0)
+    w = draw(normal((co, ci, ks, ks), 1.0 / np.sqrt(ci * ks * ks)), rng, dt)
+    b = draw(normal((co,), 0.1), rng, dt)
+    x = draw((batch, ci, hw, hw), rng, dt)
+    got = run_conv(gpu, x, w, b, stride=stride, epi=epi)
+    want = oracle.conv2d(x, w, b, stride=stride, epi=epi)
+    assert_close(got, want, TRANS if dt == np.float32 else FP16)
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_conv_scale_residual(gpu, order):
+    rng = np.random.default_rng(0)
+    ci, co, hw = 8, 16, 14
+    w = draw(normal((co, ci, 3, 3), 0.2), rng)
+    b = draw((co,), rng)
+    s = draw(uniform((co,), 0.5, 1.5), rng)
+    x = draw((1, ci, hw, hw), rng)
+    r = draw((1, co, hw, hw), rng)
+    got = run_conv(gpu, x, w, b, s, r, epi="RELU", order=order)
+    want = oracle.conv2d(x, w, b, s, r, epi="RELU", order=order)
+    assert_close(got, want, TRANS)
+
+
+def test_conv_mixed_f32_input_f16_weight(gpu):
+    rng = np.random.default_rng(0)
+    w = draw(normal((16, 8, 3, 3), 0.1), rng, np.float16)
+    x = draw((1, 8, 10, 10), rng)
+    got = run_conv(gpu, x, w)
+    assert_close(got, oracle.conv2d(x, w), FP16)
+
+
+def test_config5_yolox_conv(gpu):
+    rng = np.random.default_rng(0)
+    w = draw(normal((128, 128, 3, 3), 0.03), rng, np.float16)
+    b = draw(normal((128,), 0.02), rng, np.float16)
+    x = draw(uniform((1, 128, 80, 80), -1.0, 1.0), rng, np.float16)
+    got = run_conv(gpu, x, w, b, epi="SILU")
+    want = oracle.conv2d(x, w, b, epi="SILU")
+    assert_close(got, want, TRANS)
+
+
+def run_scores(capi, q, k, **kw):
+    dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
+    out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)
+    capi.attn_scores(out, dq, dk, **kw)
+    return out.numpy()
+
+
+@pytest.mark.parametrize("hq, hkv, tq, tkv, d, causal, span, dt", [
+    (2, 2, 64, 64, 64, True, 0, np.float16),
+    (4, 2, 100, 100, 32, True, 0, np.float16),       # GQA, ragged
+    (2, 1, 5, 37, 64, True, 0, np.float16),          # Tq < Tkv: queries align at the end
+    (2, 2, 130, 130, 16, True, 24, np.float32),      # sliding window
+    (1, 1, 70, 90, 48, False, 0, np.float32),        # no mask
+    (3, 3, 257, 257, 128, True, 0, np.float16),
+])
+def test_scores(gpu, hq, hkv, tq, tkv, d, causal, span, dt):
+    rng = np.random.default_rng(0)
+    q = draw((hq, tq, d), rng, dt)
+    k = draw((hkv, tkv, d), rng, dt)
+    got = run_scores(gpu, q, k, causal=causal, span=span)
+    want = oracle.attn_scores(q, k, causal=causal, span=span)
+    assert_close(got, want, FP32 if dt == np.float16 else TRANS)
+
+
+def test_config4_attention_scores(gpu):
+    """Q,K [8,1024,256] fp16, S = QK^T/16 causal; oracle on heads 0 and 7."""
+    rng = np.random.default_rng(0)
+    q = draw((8, 1024, 256), rng, np.float16)
+    k = draw((8, 1024, 256), rng, np.float16)
+    got = run_scores(gpu, q, k, scale=1.0 / 16, causal=True)
+    i, j = np.indices((1024, 1024))
+    assert np.isneginf(got[:, j > i]).all()
+    for h in (0, 7):
+        want = oracle.attn_scores(q[h:h + 1], k[h:h + 1], scale=1.0 / 16, causal=True)
+        assert_close(got[h:h + 1], want, FP32)

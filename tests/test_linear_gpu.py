@@ -1,0 +1,170 @@
+"""Linear through the C ABI on the MI355X vs the oracle (and float64).
+
+Cases follow the reference's own Linear tests (/root/reference/python/tests/
+nodes/test_linear.py:11-84): slab M <= 8 at the FP32 tier, tile M > 8, odd N,
+split-K, K tails, residual before/after; then BASELINE's configs 1-3.
+Draws follow node_check: default_rng(0), params (weight, bias) before inputs.
+"""
+import numpy as np
+import pytest
+
+from helpers import FP16, FP32, TRANS, assert_close, draw, max_rel_err, normal
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def run_linear(capi, x, w, b=None, r=None, out_dtype=np.float32, **kw):
+    dx, dw = capi.DeviceArray.from_numpy(x), capi.DeviceArray.from_numpy(w)
+    db = capi.DeviceArray.from_numpy(b) if b is not None else None
+    dr = capi.DeviceArray.from_numpy(r) if r is not None else None
+    N = w.shape[0] // 2 if kw.get("gated") else w.shape[0]
+    out = capi.DeviceArray(x.shape[:-1] + (N,), out_dtype)
+    capi.linear(out, dx, dw, db, dr, **kw)
+    return out.numpy()
+
+
+@pytest.mark.parametrize(
+    "m, k, n, has_bias, epi, split, tol",
+    [
+        (1, 64, 32, True, "NONE", 0, FP32),
+        (33, 64, 32, True, "NONE", 0, FP32),   # the reference reruns slab_m1 at M=33
+        (8, 96, 40, False, "NONE", 0, FP32),
+        (33, 96, 48, True, "RELU", 0, FP32),
+        (64, 128, 100, False, "GELU_TANH", 0, TRANS),
+        (16, 256, 64, True, "NONE", 64, FP32),
+        (33, 1000, 100, True, "NONE", 0, FP32),
+        (33, 100, 48, False, "NONE", 0, FP32),
+        (33, 102, 48, False, "NONE", 0, FP32),
+        (33, 101, 48, False, "NONE", 0, FP32),
+        (16, 2050, 64, True, "NONE", 0, FP32),
+        (33, 1000, 48, False, "NONE", 100, FP32),
+        (3, 101, 77, True, "SILU", 0, TRANS),
+        (200, 300, 260, True, "GELU", 0, TRANS),
+        (130, 64, 70, True, "SIGMOID", 0, TRANS),
+    ],
+)
+def test_linear_f32(gpu, m, k, n, has_bias, epi, split, tol):
+    rng = np.random.default_rng(0)
+    w = draw(normal((n, k), 1.0 / np.sqrt(k)), rng)
+    b = draw((n,), rng) if has_bias else None
+    x = draw((m, k), rng)
+    got = run_linear(gpu, x, w, b, epi=epi, split_size=split)
+    want = oracle.linear(x, w, b, epi=epi, split_size=split)
+    assert_close(got, want, tol, "vs oracle")
+    # and the float64 closed form at the reference's own tier for this path
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + (0 if b is None else b.astype(np.float64))
+    ref = oracle.epilogue(ref.astype(np.float32), epi) if epi != "NONE" else ref
+    assert_close(got, ref, FP16 if m > 8 else TRANS, "vs float64")
+    # replay is bit-identical (node_check's second forward)
+    again = run_linear(gpu, x, w, b, epi=epi, split_size=split)
+    np.testing.assert_array_equal(again, got)
+
+
+@pytest.mark.parametrize("m, order", [(4, 0), (4, 1), (33, 0), (33, 1), (64, 1)])
+def test_linear_residual(gpu, m, order):
+    k, n = 64, 48
+    rng = np.random.default_rng(0)
+    w = draw(normal((n, k), 1.0 / np.sqrt(k)), rng)
+    b = draw((n,), rng)
+    x = draw((m, k), rng)
+    r = draw((m, n), rng)
+    got = run_linear(gpu, x, w, b, r, epi="RELU", order=order)
+    want = oracle.linear(x, w, b, r, epi="RELU", order=order)
+    assert_close(got, want, FP32)
+
+
+@pytest.mark.parametrize("m, scale, rep", [(5, 0.5, True), (40, -2.0, True), (40, 0.25, False)])
+def test_linear_scale_repeat(gpu, m, scale, rep):
+    """scalarScale and [N]-repeating vs full [M,N] residual (linear.h:49-50,2333-2338)."""
+    k, n = 96, 64
+    rng = np.random.default_rng(1)
+    w = draw(normal((n, k), 0.1), rng)
+    b = draw((n,), rng)
+    x = draw((m, k), rng)
+    r = draw((n,) if rep else (m, n), rng)
+    got = run_linear(gpu, x, w, b, r, epi="SILU", scale=scale)
+    want = oracle.linear(x, w, b, r, epi="SILU", scale=scale)
+    assert_close(got, want, TRANS)
+
+
+@pytest.mark.parametrize("m, k, n, idt, wdt, odt", [
+    (1, 2048, 512, np.float16, np.float16, np.float32),
+    (8, 2048, 256, np.float16, np.float16, np.float16),
+    (5, 512, 96, np.float32, np.float16, np.float32),
+    (64, 512, 256, np.float16, np.float16, np.float32),
+    (100, 300, 130, np.float32, np.float16, np.float32),   # tile stages I as fp16
+    (70, 256, 64, np.float16, np.float32, np.float32),     # tile stages W as fp16
+    (128, 1024, 512, np.float16, np.float16, np.float16),
+])
+def test_linear_mixed_dtypes(gpu, m, k, n, idt, wdt, odt):
+    rng = np.random.default_rng(0)
+    w = draw(normal((n, k), 0.02), rng, wdt)
+    b = draw(normal((n,), 0.02), rng, wdt)
+    x = draw((m, k), rng, idt)
+    got = run_linear(gpu, x, w, b, out_dtype=odt, epi="GELU_TANH")
+    want = oracle.linear(x, w, b, epi="GELU_TANH", out_dtype=odt)
+    tol = FP16 if odt == np.float16 else TRANS
+    assert_close(got.astype(np.float32), want.astype(np.float32), tol)
+
+
+@pytest.mark.parametrize("m, k, h, split", [(8, 256, 96, 0), (64, 256, 64, 0), (300, 512, 200, 0),
+                                           (40, 4096, 64, 0), (33, 1000, 48, 100)])
+def test_linear_gated(gpu, m, k, h, split):
+    """Linear over concat(gate, up) + GatedMul(SiLU), fused (gated-feed-forward.h:37-46)."""
+    rng = np.random.default_rng(0)
+    w = draw(normal((2 * h, k), 0.05), rng, np.float16)
+    b = draw(normal((2 * h,), 0.02), rng, np.float16)
+    x = draw((m, k), rng, np.float16)
+    got = run_linear(gpu, x, w, b, gated=True, gate_epi="SILU", split_size=split)
+    y = oracle.linear(x, w, b)
+    want = oracle.gated_mul(y, epi="SILU")
+    assert_close(got, want, TRANS)
+
+
+def test_gated_mul_alone(gpu):
+    rng = np.random.default_rng(0)
+    x = draw((37, 2 * 50), rng)
+    d = gpu.DeviceArray.from_numpy(x)
+    out = gpu.DeviceArray((37, 50), np.float32)
+    gpu.gated_mul(out, d, "GELU")
+    assert_close(out.numpy(), oracle.gated_mul(x, epi="GELU"), TRANS)
+
+
+# ---- BASELINE configs ----
+
+def test_config1_gpt2_cfc(gpu):
+    """X[128,768] f32, W[768,3072]^T, bias, GELU-tanh; fp32 tier 1e-5."""
+    rng = np.random.default_rng(0)
+    w = draw(normal((768, 3072), 0.02), rng).T.copy()
+    b = draw(normal((3072,), 0.02), rng)
+    x = draw((128, 768), rng)
+    got = run_linear(gpu, x, w, b, epi="GELU_TANH")
+    want = oracle.linear(x, w, b, epi="GELU_TANH")
+    assert_close(got, want, FP32)
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_config2_decode_gemv(gpu, m):
+    rng = np.random.default_rng(0)
+    w = draw(normal((2048, 8192), 0.02), rng, np.float16).T.copy()
+    x = draw((m, 2048), rng, np.float16)
+    got = run_linear(gpu, x, w)
+    want = oracle.linear(x, w)
+    assert_close(got, want, FP32)
+
+
+def test_config3_prefill_gate_up(gpu):
+    """X[2048,3072], concat(W_gate, W_up) -> [16384, 3072], SiLU(g)*u, fp32 out.
+    The oracle checks a sample of 48 rows at full size."""
+    rng = np.random.default_rng(0)
+    wg = draw(normal((3072, 8192), 0.02), rng, np.float16).T
+    wu = draw(normal((3072, 8192), 0.02), rng, np.float16).T
+    w = np.ascontiguousarray(np.concatenate([wg, wu], axis=0))
+    x = draw((2048, 3072), rng, np.float16)
+    got = run_linear(gpu, x, w, gated=True, gate_epi="SILU")
+    assert np.isfinite(got).all()
+    rows = np.random.default_rng(5).choice(2048, 48, replace=False)
+    rows[:2] = [0, 2047]
+    want = oracle.gated_mul(oracle.linear(x[rows], w, stage="tile"), epi="SILU")
+    assert_close(got[rows], want, TRANS)

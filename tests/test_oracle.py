@@ -1,0 +1,231 @@
+"""Pins the CPU oracle (oracle/vai_oracle.c) before anything is compared to it.
+
+Every check is independent of the oracle's own formulas: numpy's IEEE
+float16, float64 closed forms written differently (einsum, explicit padding,
+np.triu masks), brute-force bounds on fp32 accumulation error, and shapes
+chosen so a transposed operand, a wrong bias/residual index, a swapped
+residual order or a dropped scale fails.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+EPS32 = np.finfo(np.float32).eps
+
+
+# ---- fp16 conversion: /root/reference/vai/engine/tensor.cpp:42-90 ----------
+
+def test_half_to_float_all_codes():
+    codes = np.arange(65536, dtype=np.uint16)
+    got = oracle.from_f16(codes.view(np.float16))
+    want = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_float_to_half_normal_range_is_ieee_rne():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(1 << 18) * np.exp(rng.uniform(-9, 10, 1 << 18))).astype(np.float32)
+    x = x[(np.abs(x) >= 6.104e-5) & (np.abs(x) < 65504)]
+    # ties: exact midpoints between neighbouring halves round to even
+    h = np.arange(0x0400, 0x7BFF, 7, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mid = (h + np.nextafter(h.astype(np.float16), np.float16(np.inf)).astype(np.float32)) / 2
+    for v in (x, mid, -mid):
+        assert np.array_equal(oracle.to_f16(v).view(np.uint16), v.astype(np.float16).view(np.uint16))
+
+
+def test_float_to_half_flushes_subnormals_and_saturates():
+    tiny = np.array([6.0e-5, 1e-7, -3e-6, 5.96e-8], np.float32)
+    assert np.array_equal(oracle.to_f16(tiny).view(np.uint16), np.array([0, 0, 0x8000, 0], np.uint16))
+    big = np.array([65520.0, 1e6, -1e9, np.inf], np.float32)
+    assert np.array_equal(oracle.to_f16(big).view(np.uint16), np.array([0x7C00, 0x7C00, 0xFC00, 0x7C00], np.uint16))
+    assert np.isnan(oracle.to_f16(np.array([np.nan], np.float32))).all()
+    assert oracle.to_f16(np.array([65504.0], np.float32)).view(np.uint16)[0] == 0x7BFF
+
+
+# ---- epilogues: /root/reference/vai/shaders/common/activation.h:19-58 -------
+
+X = np.concatenate([np.linspace(-12, 12, 2001), [0.0, 1e-3, -1e-3, 3.0, -3.0]]).astype(np.float32)
+
+
+def _closed(epi, x):
+    x = x.astype(np.float64)
+    erf = np.vectorize(math.erf)
+    return {
+        "NONE": x,
+        "RELU": np.maximum(x, 0),
+        "GELU": 0.5 * x * (1 + erf(x / math.sqrt(2))),
+        "GELU_TANH": 0.5 * x * (1 + np.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3))),
+        "SILU": x / (1 + np.exp(-x)),
+        "SIGMOID": 1 / (1 + np.exp(-x)),
+    }[epi]
+
+
+@pytest.mark.parametrize("epi", list(oracle.EPILOGUES))
+def test_epilogue_closed_forms(epi):
+    got = oracle.epilogue(X, epi).astype(np.float64)
+    want = _closed(epi, X)
+    # A&S 7.1.26 is within 1.5e-7 of erf; the rest is fp32 rounding.
+    err = np.abs(got - want)
+    assert (err <= 2e-6 * np.abs(want) + 2e-7 * (1 + np.abs(X))).all(), float(err.max())
+
+
+def test_epilogue_special_points():
+    z = np.zeros(1, np.float32)
+    for epi in ("RELU", "GELU", "GELU_TANH", "SILU"):
+        assert oracle.epilogue(z, epi)[0] == 0.0
+    assert oracle.epilogue(z, "SIGMOID")[0] == 0.5
+    assert oracle.epilogue(np.array([-5.0], np.float32), "RELU")[0] == 0.0
+    # GELU(x) -> x for large x, -> 0 for very negative x
+    assert abs(oracle.epilogue(np.array([8.0], np.float32), "GELU")[0] - 8.0) < 1e-6
+    assert abs(oracle.epilogue(np.array([-8.0], np.float32), "GELU_TANH")[0]) < 1e-6
+
+
+# ---- Linear -----------------------------------------------------------------
+
+def _bound(x, w):
+    """|fp32 dot - exact| <= gamma_K * sum |x w| (Higham), plus operand rounding."""
+    k = x.shape[-1]
+    return 1.01 * k * EPS32 * (np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T) + 1e-30
+
+
+@pytest.mark.parametrize("m, k, n", [(1, 7, 5), (3, 64, 9), (12, 33, 17), (40, 130, 3)])
+@pytest.mark.parametrize("idt, wdt", [(np.float32, np.float32), (np.float16, np.float16),
+                                      (np.float32, np.float16)])
+def test_linear_plain_vs_float64(m, k, n, idt, wdt):
+    rng = np.random.default_rng(m * 1000 + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x16, w16 = x.astype(idt), w.astype(wdt)
+    for stage in ("slab", "tile"):
+        got = oracle.linear(x16, w16, stage=stage).astype(np.float64)
+        xs, ws = x16.astype(np.float32), w16.astype(np.float32)
+        if stage == "tile" and not (idt == np.float32 and wdt == np.float32):
+            xs, ws = xs.astype(np.float16).astype(np.float32), ws.astype(np.float16).astype(np.float32)
+        exact = xs.astype(np.float64) @ ws.astype(np.float64).T
+        assert (np.abs(got - exact) <= _bound(xs, ws)).all(), stage
+    if idt != wdt:   # the tile contract really rounds the fp32 side: the results differ
+        assert not np.array_equal(oracle.linear(x16, w16, stage="slab"), oracle.linear(x16, w16, stage="tile"))
+
+
+def test_linear_bias_residual_scale_orders():
+    rng = np.random.default_rng(3)
+    m, k, n = 6, 20, 10
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    r = rng.standard_normal((m, n)).astype(np.float32)
+    y = x.astype(np.float64) @ w.astype(np.float64).T + b
+    tol = dict(rtol=1e-5, atol=1e-5)
+    after = oracle.linear(x, w, b, r, epi="RELU", order=0, scale=0.5)
+    before = oracle.linear(x, w, b, r, epi="RELU", order=1, scale=0.5)
+    np.testing.assert_allclose(after, 0.5 * np.maximum(y, 0) + r, **tol)
+    np.testing.assert_allclose(before, 0.5 * np.maximum(y + r, 0), **tol)
+    assert not np.allclose(after, before)
+    # bias [M,N] vs [N] repeating; residual repeating rows
+    bfull = np.tile(b, (m, 1))
+    np.testing.assert_array_equal(oracle.linear(x, w, bfull), oracle.linear(x, w, b))
+    rrow = r[0].copy()
+    np.testing.assert_allclose(oracle.linear(x, w, None, rrow), y - b + rrow, **tol)
+
+
+def test_linear_split_matches_reduce():
+    rng = np.random.default_rng(4)
+    m, k, n, span = 9, 100, 7, 32
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    parts = np.stack([oracle.linear(x[:, s:s + span], w[:, s:s + span], stage="tile")
+                      for s in range(0, k, span)])
+    red = oracle.linear_reduce(parts, b, epi="GELU")
+    direct = oracle.linear(x, w, b, epi="GELU", stage="tile", split_size=span)
+    np.testing.assert_array_equal(red, direct)
+    exact = oracle.epilogue((x.astype(np.float64) @ w.astype(np.float64).T + b).astype(np.float32), "GELU")
+    np.testing.assert_allclose(direct, exact, rtol=1e-5, atol=1e-5)
+
+
+def test_gated_mul_closed_form():
+    rng = np.random.default_rng(5)
+    y = rng.standard_normal((4, 2 * 11)).astype(np.float32)
+    g, u = y[:, :11].astype(np.float64), y[:, 11:].astype(np.float64)
+    np.testing.assert_allclose(oracle.gated_mul(y, epi="SILU"), g / (1 + np.exp(-g)) * u, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(oracle.gated_mul(y, epi="NONE"), g * u, rtol=1e-6, atol=1e-7)
+
+
+# ---- Convolution ------------------------------------------------------------
+
+def _conv_ref(x, w, stride):
+    """float64 cross-correlation through explicit zero padding and einsum."""
+    x = x.astype(np.float64)
+    w = w.astype(np.float64)
+    co, ci, k, _ = w.shape
+    p = k // 2
+    xp = np.pad(x, [(0, 0)] * (x.ndim - 2) + [(p, p), (p, p)])
+    hi, wi = x.shape[-2:]
+    ho, wo = (hi - 1) // stride + 1, (wi - 1) // stride + 1
+    out = np.zeros(x.shape[:-3] + (co, ho, wo))
+    for kh in range(k):
+        for kw in range(k):
+            patch = xp[..., kh:kh + stride * (ho - 1) + 1:stride, kw:kw + stride * (wo - 1) + 1:stride]
+            out += np.einsum("oc,...chw->...ohw", w[:, :, kh, kw], patch)
+    return out
+
+
+@pytest.mark.parametrize("ci, co, k, s, h, w_, batch", [
+    (3, 4, 3, 1, 7, 9, 1), (5, 2, 1, 1, 4, 4, 2), (2, 3, 5, 2, 9, 6, 1), (4, 4, 3, 2, 8, 8, 3), (1, 1, 3, 1, 1, 1, 1)])
+def test_conv_vs_float64(ci, co, k, s, h, w_, batch):
+    rng = np.random.default_rng(ci * 7 + k)
+    x = rng.standard_normal((batch, ci, h, w_)).astype(np.float32)
+    w = rng.standard_normal((co, ci, k, k)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32)
+    got = oracle.conv2d(x, w, b, stride=s).astype(np.float64)
+    want = _conv_ref(x, w, s) + b[:, None, None]
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_conv_scale_residual_and_fp16_staging():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((1, 3, 6, 6)).astype(np.float32)
+    w = rng.standard_normal((4, 3, 3, 3)).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    sc = rng.uniform(0.5, 2, 4).astype(np.float32)
+    r = rng.standard_normal((1, 4, 6, 6)).astype(np.float32)
+    base = _conv_ref(x, w, 1) * sc[:, None, None] + b[:, None, None]
+    np.testing.assert_allclose(oracle.conv2d(x, w, b, sc, r, epi="RELU", order=0), np.maximum(base, 0) + r,
+                               rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(oracle.conv2d(x, w, b, sc, r, epi="RELU", order=1), np.maximum(base + r, 0),
+                               rtol=1e-5, atol=1e-5)
+    # fp16 weights stage the fp32 input as fp16 (conv-k3s1-implicit-gemm.comp writeB)
+    w16 = w.astype(np.float16)
+    got = oracle.conv2d(x, w16).astype(np.float64)
+    want = _conv_ref(x.astype(np.float16), w16, 1)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+# ---- Attention scores -------------------------------------------------------
+
+@pytest.mark.parametrize("hq, hkv, tq, tkv, d, causal, span", [
+    (2, 2, 9, 9, 8, True, 0), (4, 2, 5, 12, 16, True, 0), (2, 1, 10, 10, 4, True, 3), (1, 1, 6, 4, 8, False, 0)])
+def test_scores_vs_float64(hq, hkv, tq, tkv, d, causal, span):
+    rng = np.random.default_rng(hq + tq)
+    q = rng.standard_normal((hq, tq, d)).astype(np.float32)
+    k = rng.standard_normal((hkv, tkv, d)).astype(np.float32)
+    got = oracle.attn_scores(q, k, scale=0.25, causal=causal, span=span)
+    kk = np.repeat(k.astype(np.float64), hq // hkv, axis=0)
+    s = np.einsum("hid,hjd->hij", q.astype(np.float64), kk) * 0.25
+    off = tkv - tq
+    hide = np.zeros((tq, tkv), bool)
+    if causal:
+        hide |= np.triu(np.ones((tq, tkv), bool), k=off + 1)
+    if span:
+        pos = np.arange(tq)[:, None] + off
+        j = np.arange(tkv)[None, :]
+        hide |= (pos >= span) & (j < pos + 1 - span)
+    s[:, hide] = -np.inf
+    assert np.array_equal(np.isneginf(got), np.isneginf(s))
+    fin = ~np.isneginf(s)
+    np.testing.assert_allclose(got[fin], s[fin], rtol=1e-5, atol=1e-5)

@@ -1,0 +1,315 @@
+// capi.cpp -- the extern "C" boundary (include/vai_amd.h): argument checks,
+// kernel selection by shape and dtype, and the device-memory helpers.
+//
+// Selection replaces the reference's per-vendor tables (selectLinearTile,
+// /root/reference/vai/nodes/linear.h:2101-2119; selectConvPlan,
+// /root/reference/vai/nodes/convolution.h:5408-5443) with one rule set for
+// gfx950: M <= 8 streams W through the slab GEMV (linear.h:320), larger M
+// takes the MFMA GEMM with the largest tile that still gives the 256 CUs at
+// least one workgroup each, and split-K when even the smallest tile leaves
+// most CUs idle and K is long.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+#include <algorithm>
+#include "../../include/vai_amd.h"
+#include "kernels.h"
+
+using namespace vai_dev;
+
+namespace {
+
+constexpr uint32_t kCUs = 256;
+
+bool dtype_ok(int32_t d) { return d == VAI_DTYPE_F32 || d == VAI_DTYPE_F16; }
+size_t dtype_bytes(int32_t d) { return d == VAI_DTYPE_F16 ? 2 : 4; }
+vai_status hip_status(hipError_t e) { return e == hipSuccess ? VAI_OK : (vai_status)e; }
+
+struct LinearPlan {
+    enum Kind { Slab, SlabThenGate, Tile } kind;
+    GemmTile tile;
+    uint32_t bm, bn;
+    uint32_t split_size, splits;
+    size_t workspace;
+};
+
+uint32_t tiles_of(uint32_t M, uint32_t N, uint32_t bm, uint32_t bn)
+{
+    return ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+}
+
+vai_status check_linear(const vai_linear_args* a)
+{
+    if (!a || !a->out || !a->in || !a->weight) return VAI_ERR_INVALID_ARG;
+    if (a->M == 0 || a->N == 0 || a->K == 0) return VAI_ERR_SHAPE;
+    if (!dtype_ok(a->o_dtype) || !dtype_ok(a->i_dtype) || !dtype_ok(a->w_dtype)) return VAI_ERR_DTYPE;
+    if (a->bias && !dtype_ok(a->b_dtype)) return VAI_ERR_DTYPE;
+    if (a->epilogue > VAI_EPI_SIGMOID || a->residual_order > 1) return VAI_ERR_INVALID_ARG;
+    const uint64_t MN = (uint64_t)a->M * a->N;
+    if (a->bias && a->bias_repeat && (a->bias_repeat % a->N != 0 || MN % a->bias_repeat != 0)) return VAI_ERR_SHAPE;
+    if (a->residual && a->residual_repeat && (a->residual_repeat % a->N != 0 || MN % a->residual_repeat != 0))
+        return VAI_ERR_SHAPE;
+    if (a->split_size && a->split_size < 32) return VAI_ERR_INVALID_ARG;
+    if (a->gated) {
+        if (a->N % 2 != 0 || a->gate_epilogue > VAI_EPI_SIGMOID) return VAI_ERR_SHAPE;
+        if (a->epilogue != VAI_EPI_NONE || a->residual || a->scalar_scale != 1.0f) return VAI_ERR_UNSUPPORTED;
+        if (a->bias && a->bias_repeat != a->N) return VAI_ERR_UNSUPPORTED;   // a [2H] bias row only
+    }
+    return VAI_OK;
+}
+
+LinearPlan plan_linear(const vai_linear_args* a)
+{
+    LinearPlan p{};
+    const uint32_t M = a->M, N = a->N, K = a->K;
+    if (M <= 8) {
+        p.kind = a->gated ? LinearPlan::SlabThenGate : LinearPlan::Slab;
+        p.splits = 1;
+        p.split_size = K;
+        p.workspace = a->gated ? (size_t)M * N * 4 : 0;
+        return p;
+    }
+    p.kind = LinearPlan::Tile;
+    const bool f32 = a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32;
+    const uint32_t bk = f32 ? 16 : 32;
+    // Candidate tiles, largest first (the gated kernel pairs fragments, so its
+    // smallest N tile is 128 columns = 64 output columns).
+    struct Cand { GemmTile t; uint32_t bm, bn; };
+    const Cand cands[] = {
+        {GemmTile::T256x128, 256, 128}, {GemmTile::T128x128, 128, 128},
+        {GemmTile::T128x64, 128, a->gated ? 128u : 64u}, {GemmTile::T64x64, 64, a->gated ? 128u : 64u},
+    };
+    const uint32_t ncols = N;   // gated: 2H logical columns
+    Cand pick = cands[3];
+    for (const Cand& c : cands) {
+        if (f32 && c.bm == 256) continue;   // fp32 staging keeps 128-row tiles (LDS, registers)
+        if (tiles_of(M, ncols, c.bm, c.bn) >= kCUs) { pick = c; break; }
+    }
+    p.tile = pick.t;
+    p.bm = pick.bm;
+    p.bn = pick.bn;
+    const uint32_t tiles = tiles_of(M, ncols, pick.bm, pick.bn);
+    if (a->split_size) {
+        p.split_size = a->split_size;
+        p.splits = (K + a->split_size - 1) / a->split_size;
+    } else {
+        uint32_t splits = 1;
+        if (tiles < kCUs / 2 && K >= 1024) {
+            splits = std::min<uint32_t>((kCUs + tiles - 1) / tiles, K / 256);
+            splits = std::max<uint32_t>(splits, 1);
+        }
+        p.split_size = splits > 1 ? ((K + splits - 1) / splits + bk - 1) / bk * bk : K;
+        p.splits = (K + p.split_size - 1) / p.split_size;
+    }
+    p.workspace = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
+    return p;
+}
+
+const char* tile_name(GemmTile t, bool gated)
+{
+    switch (t) {
+    case GemmTile::T64x64: return gated ? "64x128" : "64x64";
+    case GemmTile::T128x64: return gated ? "128x128" : "128x64";
+    case GemmTile::T128x128: return "128x128";
+    default: return "256x128";
+    }
+}
+
+}   // namespace
+
+extern "C" {
+
+size_t vai_linear_workspace_size(const vai_linear_args* a)
+{
+    if (check_linear(a) != VAI_OK) return 0;
+    return plan_linear(a).workspace;
+}
+
+vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len, uint32_t* split_count)
+{
+    const vai_status st = check_linear(a);
+    if (st != VAI_OK) return st;
+    const LinearPlan p = plan_linear(a);
+    char buf[64];
+    if (p.kind != LinearPlan::Tile) {
+        SlabParams sp{};
+        sp.K = a->K; sp.w_dtype = a->w_dtype; sp.i_dtype = a->i_dtype; sp.weight = a->weight; sp.in = a->in;
+        snprintf(buf, sizeof buf, "%s%s", slab_vec_ok(sp) ? "slab" : "slab_scalar",
+                 p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
+    } else {
+        const bool f32 = a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32;
+        snprintf(buf, sizeof buf, "tile_%s_%s%s", f32 ? "f32" : "f16", tile_name(p.tile, a->gated),
+                 a->gated ? "_gated" : "");
+    }
+    if (name && name_len) { strncpy(name, buf, name_len - 1); name[name_len - 1] = 0; }
+    if (split_count) *split_count = p.splits;
+    return VAI_OK;
+}
+
+vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
+{
+    vai_status st = check_linear(a);
+    if (st != VAI_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    const LinearPlan p = plan_linear(a);
+    if (p.workspace && (!a->workspace || a->workspace_bytes < p.workspace)) return VAI_ERR_WORKSPACE;
+
+    if (p.kind != LinearPlan::Tile) {
+        SlabParams sp{};
+        sp.in = a->in; sp.weight = a->weight; sp.bias = a->bias; sp.residual = a->residual;
+        sp.M = a->M; sp.N = a->N; sp.K = a->K;
+        sp.i_dtype = a->i_dtype; sp.w_dtype = a->w_dtype; sp.b_dtype = a->b_dtype;
+        sp.epilogue = a->epilogue; sp.residual_order = a->residual_order;
+        sp.bias_repeat = a->bias_repeat; sp.residual_repeat = a->residual_repeat;
+        sp.scalar_scale = a->scalar_scale;
+        if (p.kind == LinearPlan::Slab) {
+            sp.out = a->out; sp.o_dtype = a->o_dtype;
+            return hip_status(slab_launch(sp, s));
+        }
+        // Gated at M <= 8: the fp32 Linear output, then the gating pass.
+        sp.out = a->workspace; sp.o_dtype = VAI_DTYPE_F32;
+        hipError_t e = slab_launch(sp, s);
+        if (e != hipSuccess) return hip_status(e);
+        return hip_status(gated_mul_launch(a->out, a->o_dtype, a->workspace, VAI_DTYPE_F32, a->M, a->N / 2,
+                                           a->gate_epilogue, s));
+    }
+
+    GemmParams g{};
+    g.A = a->in; g.B = a->weight;
+    g.a_dtype = a->i_dtype; g.b_dtype = a->w_dtype;
+    g.M = a->M; g.N = a->N; g.K = a->K;
+    g.batch = 1; g.b_group = 1;
+    g.split_size = p.split_size; g.splits = p.splits;
+    g.bias = a->bias; g.bias_dtype = a->b_dtype; g.bias_repeat = a->bias_repeat;
+    g.residual = a->residual; g.residual_dtype = a->o_dtype; g.residual_repeat = a->residual_repeat;
+    g.epilogue = a->gated ? a->gate_epilogue : a->epilogue;
+    g.residual_order = a->residual_order; g.scalar_scale = a->scalar_scale;
+    g.H = a->gated ? a->N / 2 : 0;
+    if (p.splits > 1) { g.C = a->workspace; g.c_dtype = VAI_DTYPE_F32; }
+    else { g.C = a->out; g.c_dtype = a->o_dtype; }
+    hipError_t e = gemm_launch(g, a->gated ? BKind::Gated : BKind::Dense,
+                               a->gated ? EpiKind::Gated : EpiKind::Linear, p.tile, s);
+    if (e != hipSuccess || p.splits == 1) return hip_status(e);
+    const size_t MN = (size_t)a->M * (a->gated ? a->N / 2 : a->N);
+    return hip_status(linear_reduce_launch(a->out, a->o_dtype, (const float*)a->workspace, p.splits, MN,
+                                           a->bias, a->b_dtype, a->bias_repeat, a->residual, a->residual_repeat,
+                                           a->epilogue, a->residual_order, a->scalar_scale,
+                                           a->gated ? a->N / 2 : 0, a->gate_epilogue, a->N, s));
+}
+
+vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int32_t i_dtype, uint32_t rows,
+                                uint32_t H, uint32_t epilogue, vai_stream_t stream)
+{
+    if (!out || !in) return VAI_ERR_INVALID_ARG;
+    if (!dtype_ok(o_dtype) || !dtype_ok(i_dtype)) return VAI_ERR_DTYPE;
+    if (rows == 0 || H == 0) return VAI_ERR_SHAPE;
+    if (epilogue > VAI_EPI_SIGMOID) return VAI_ERR_INVALID_ARG;
+    return hip_status(gated_mul_launch(out, o_dtype, in, i_dtype, rows, H, epilogue, (hipStream_t)stream));
+}
+
+vai_status vai_conv2d_launch(const vai_conv2d_args* a, vai_stream_t stream)
+{
+    if (!a || !a->out || !a->in || !a->weight) return VAI_ERR_INVALID_ARG;
+    if (!dtype_ok(a->o_dtype) || !dtype_ok(a->i_dtype) || !dtype_ok(a->w_dtype)) return VAI_ERR_DTYPE;
+    // fp16 activations and fp16 outputs need fp16 weights (convolution.h:4140-4142).
+    if (a->w_dtype == VAI_DTYPE_F32 && (a->i_dtype == VAI_DTYPE_F16 || a->o_dtype == VAI_DTYPE_F16))
+        return VAI_ERR_DTYPE;
+    if (a->batch == 0 || a->ci == 0 || a->co == 0 || a->hi == 0 || a->wi == 0 || a->stride == 0)
+        return VAI_ERR_SHAPE;
+    if (a->kernel == 0 || a->kernel % 2 == 0) return VAI_ERR_SHAPE;
+    if (a->epilogue > VAI_EPI_SIGMOID || a->residual_order > 1) return VAI_ERR_INVALID_ARG;
+    const uint32_t ho = (a->hi - 1) / a->stride + 1, wo = (a->wi - 1) / a->stride + 1;
+    GemmParams g{};
+    g.A = a->weight; g.B = a->in; g.C = a->out;
+    g.a_dtype = a->w_dtype; g.b_dtype = a->i_dtype; g.c_dtype = a->o_dtype;
+    g.M = a->co; g.N = ho * wo; g.K = a->ci * a->kernel * a->kernel;
+    g.batch = a->batch; g.b_group = 1;
+    g.a_batch_stride = 0;
+    g.b_batch_stride = (size_t)a->ci * a->hi * a->wi;
+    g.c_batch_stride = (size_t)a->co * ho * wo;
+    g.split_size = g.K; g.splits = 1;
+    g.bias = a->bias; g.bias_dtype = a->w_dtype; g.conv_scale = a->scale;
+    g.residual = a->residual; g.residual_dtype = a->i_dtype;
+    g.epilogue = a->epilogue; g.residual_order = a->residual_order; g.scalar_scale = 1.f;
+    g.ci = a->ci; g.hi = a->hi; g.wi = a->wi; g.wo = wo; g.ks = a->kernel; g.stride = a->stride;
+    const GemmTile t = tiles_of(g.M, g.N, 128, 64) * a->batch >= kCUs ? GemmTile::T128x64 : GemmTile::T64x64;
+    return hip_status(gemm_launch(g, BKind::Im2col, EpiKind::Conv, t, (hipStream_t)stream));
+}
+
+vai_status vai_attn_scores_launch(const vai_attn_scores_args* a, vai_stream_t stream)
+{
+    if (!a || !a->scores || !a->q || !a->k) return VAI_ERR_INVALID_ARG;
+    if (!dtype_ok(a->dtype)) return VAI_ERR_DTYPE;
+    if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || a->tkv == 0 || a->head_dim == 0)
+        return VAI_ERR_SHAPE;
+    if (a->hq % a->hkv != 0) return VAI_ERR_SHAPE;
+    GemmParams g{};
+    g.A = a->q; g.B = a->k; g.C = a->scores;
+    g.a_dtype = a->dtype; g.b_dtype = a->dtype; g.c_dtype = VAI_DTYPE_F32;
+    g.M = a->tq; g.N = a->tkv; g.K = a->head_dim;
+    g.batch = a->batch * a->hq; g.b_group = a->hq / a->hkv;
+    g.a_batch_stride = (size_t)a->tq * a->head_dim;
+    g.b_batch_stride = (size_t)a->tkv * a->head_dim;
+    g.c_batch_stride = (size_t)a->tq * a->tkv;
+    g.split_size = g.K; g.splits = 1;
+    g.scalar_scale = a->scale; g.causal = a->causal; g.span = a->span;
+    g.causal_offset = (int32_t)a->tkv - (int32_t)a->tq;
+    const GemmTile t = tiles_of(g.M, g.N, 128, 128) * g.batch >= kCUs ? GemmTile::T128x128 : GemmTile::T64x64;
+    return hip_status(gemm_launch(g, BKind::Dense, EpiKind::Scores, t, (hipStream_t)stream));
+}
+
+// ---- device memory / streams / events ----
+vai_status vai_device_count(int* count) { return hip_status(hipGetDeviceCount(count)); }
+vai_status vai_set_device(int device) { return hip_status(hipSetDevice(device)); }
+vai_status vai_malloc(void** ptr, size_t bytes) { return hip_status(hipMalloc(ptr, bytes)); }
+vai_status vai_free(void* ptr) { return hip_status(hipFree(ptr)); }
+vai_status vai_memcpy_h2d(void* dst, const void* src, size_t bytes, vai_stream_t s)
+{
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)s);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)s);
+    return hip_status(e);
+}
+vai_status vai_memcpy_d2h(void* dst, const void* src, size_t bytes, vai_stream_t s)
+{
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)s);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)s);
+    return hip_status(e);
+}
+vai_status vai_memcpy_d2d(void* dst, const void* src, size_t bytes, vai_stream_t s)
+{
+    return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)s));
+}
+vai_status vai_memset(void* dst, int value, size_t bytes, vai_stream_t s)
+{
+    return hip_status(hipMemsetAsync(dst, value, bytes, (hipStream_t)s));
+}
+vai_status vai_stream_create(vai_stream_t* s) { return hip_status(hipStreamCreate((hipStream_t*)s)); }
+vai_status vai_stream_destroy(vai_stream_t s) { return hip_status(hipStreamDestroy((hipStream_t)s)); }
+vai_status vai_stream_sync(vai_stream_t s) { return hip_status(hipStreamSynchronize((hipStream_t)s)); }
+vai_status vai_device_sync(void) { return hip_status(hipDeviceSynchronize()); }
+vai_status vai_event_create(vai_event_t* ev) { return hip_status(hipEventCreate((hipEvent_t*)ev)); }
+vai_status vai_event_destroy(vai_event_t ev) { return hip_status(hipEventDestroy((hipEvent_t)ev)); }
+vai_status vai_event_record(vai_event_t ev, vai_stream_t s)
+{
+    return hip_status(hipEventRecord((hipEvent_t)ev, (hipStream_t)s));
+}
+vai_status vai_event_sync(vai_event_t ev) { return hip_status(hipEventSynchronize((hipEvent_t)ev)); }
+vai_status vai_event_elapsed_ms(float* ms, vai_event_t a, vai_event_t b)
+{
+    return hip_status(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+}
+
+const char* vai_status_string(vai_status s)
+{
+    switch ((int)s) {
+    case VAI_OK: return "ok";
+    case VAI_ERR_INVALID_ARG: return "invalid argument";
+    case VAI_ERR_SHAPE: return "shape mismatch";
+    case VAI_ERR_DTYPE: return "unsupported dtype combination";
+    case VAI_ERR_WORKSPACE: return "workspace missing or too small";
+    case VAI_ERR_UNSUPPORTED: return "unsupported configuration";
+    default: return hipGetErrorString((hipError_t)s);
+    }
+}
+
+}   // extern "C"

@@ -1,0 +1,63 @@
+// device_common.h -- dtype access and epilogue math shared by the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vai_dev {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+enum : int { DT_F32 = 0, DT_F16 = 1 };
+
+__device__ __forceinline__ float ld(const void* p, int dt, size_t i)
+{
+    return dt == DT_F16 ? (float)((const half_t*)p)[i] : ((const float*)p)[i];
+}
+__device__ __forceinline__ void st(void* p, int dt, size_t i, float v)
+{
+    if (dt == DT_F16) ((half_t*)p)[i] = (half_t)v;   // round-to-nearest-even
+    else ((float*)p)[i] = v;
+}
+
+// Epilogues of vai::Epilogue, as the reference's activation.h states them
+// (/root/reference/vai/shaders/common/activation.h:19-58): GELU (erf) through
+// Abramowitz-Stegun 7.1.26, GELU-tanh, SiLU, sigmoid.
+__device__ __forceinline__ float erf_as(float x)
+{
+    const float t = 1.0f / (1.0f + 0.3275911f * fabsf(x));
+    const float p = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t
+                     + 0.254829592f) * t;
+    const float s = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
+    return s * (1.0f - p * expf(-x * x));
+}
+
+__device__ __forceinline__ float epilogue(float x, uint32_t epi)
+{
+    switch (epi) {
+    case 1: return x > 0.f ? x : 0.f;
+    case 2: return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
+    case 3: return 0.5f * x * (1.0f + tanhf(0.79788456080286535f * (x + 0.044715f * x * x * x)));
+    case 4: return x / (1.0f + expf(-x));
+    case 5: return 1.0f / (1.0f + expf(-x));
+    default: return x;
+    }
+}
+
+// s * epi(acc + r) (before) or s * epi(acc) + r (after): linear-slab.comp:236-242.
+__device__ __forceinline__ float finish(float acc, float r, uint32_t epi, uint32_t order, float s)
+{
+    return order == 1 ? s * epilogue(acc + r, epi) : s * epilogue(acc, epi) + r;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}   // namespace vai_dev

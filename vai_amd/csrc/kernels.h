@@ -1,0 +1,85 @@
+// kernels.h -- host-visible launch entry points of the gfx950 kernels (internal
+// to libvai_amd; the public surface is include/vai_amd.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vai_dev {
+
+struct SlabParams {
+    void* out;
+    const void* in;
+    const void* weight;
+    const void* bias;
+    const void* residual;
+    uint32_t M, N, K;
+    int o_dtype, i_dtype, w_dtype, b_dtype;
+    uint32_t epilogue, residual_order, bias_repeat, residual_repeat;
+    float scalar_scale;
+};
+bool slab_vec_ok(const SlabParams& a);
+hipError_t slab_launch(const SlabParams& a, hipStream_t s);
+
+// The operand a GEMM's "B" side reads: C[M,N] = A[M,K] . B[N,K]^T.
+enum class BKind : int {
+    Dense = 0,   // B rows are rows of a row-major [N, K] matrix
+    Gated = 1,   // logical column pairs (j, H + j) of a [2H, K] matrix
+    Im2col = 2,  // B[p, k] gathered from an NCHW image (implicit-GEMM conv)
+};
+
+// What the GEMM does with its accumulators.
+enum class EpiKind : int {
+    Linear = 0,    // bias / epilogue / residual / scale, or a split-K partial
+    Gated = 1,     // gate_epi(g + bg) * (u + bu) into O[M, H]
+    Scores = 2,    // scale, causal mask -> -inf, fp32 out
+    Conv = 3,      // per-row (channel) scale / bias, epilogue, residual
+};
+
+struct GemmParams {
+    // A [M, K] row-major (lda = K), B per BKind, C per EpiKind.
+    const void* A;
+    const void* B;
+    void* C;
+    int a_dtype, b_dtype, c_dtype;
+    uint32_t M, N, K;
+    // batching over blockIdx.z: element strides per batch entry
+    uint32_t batch;
+    size_t a_batch_stride, b_batch_stride, c_batch_stride;
+    uint32_t b_group;             // B batch index = z / b_group (GQA)
+    // split-K: span per split; splits > 1 writes fp32 partials to C + z*M*N
+    uint32_t split_size, splits;
+    // Linear / Gated epilogue
+    const void* bias;
+    int bias_dtype;
+    uint32_t bias_repeat;
+    const void* residual;
+    int residual_dtype;
+    uint32_t residual_repeat;
+    uint32_t epilogue, residual_order;
+    float scalar_scale;
+    uint32_t H;                   // Gated: half width of W
+    // Scores
+    uint32_t causal, span;
+    int32_t causal_offset;        // Tkv - Tq
+    // Conv: image geometry (B side is the gathered input)
+    const void* conv_scale;
+    uint32_t ci, hi, wi, wo, ks, stride;
+};
+
+// The tile shapes the launcher offers.
+enum class GemmTile : int { T64x64 = 0, T128x64 = 1, T128x128 = 2, T256x128 = 3 };
+
+hipError_t gemm_launch(const GemmParams& p, BKind bk, EpiKind ek, GemmTile tile, hipStream_t s);
+
+// Split-K fold for Linear: O = s*epi(sum_z P[z] + B) (+R).
+hipError_t linear_reduce_launch(void* out, int o_dtype, const float* partials, uint32_t splits, size_t MN,
+                                const void* bias, int b_dtype, uint32_t bias_repeat,
+                                const void* residual, uint32_t residual_repeat,
+                                uint32_t epi, uint32_t order, float s, uint32_t gated_H, uint32_t gate_epi,
+                                uint32_t N, hipStream_t st);
+
+hipError_t gated_mul_launch(void* out, int o_dtype, const void* in, int i_dtype, uint32_t rows, uint32_t H,
+                            uint32_t epi, hipStream_t s);
+
+}   // namespace vai_dev

@@ -1,0 +1,198 @@
+// slab.hip -- Linear for M <= 8: the HBM-streaming GEMV (the role of
+// /root/reference/vai/shaders/linear-slab.comp).
+//
+// O[m,n] = s * epi(sum_k I[m,k] W[n,k] + B) (+R), fp32 accumulation on the
+// operands as stored (fp16 is exact in fp32), as linear-slab.comp:5-15 states.
+//
+// Design (gfx950): W dominates the traffic (N*K elements, read once), so the
+// kernel is shaped for HBM: each wave owns R whole rows of W and issues all
+// of its 16-byte non-temporal loads for a K block before touching them, so a
+// CU keeps ~100 KB of loads in flight. The M <= 8 input rows are staged once
+// per workgroup in LDS and broadcast to the four waves. Each lane ends with
+// M*R partial dot products; a butterfly over the wave halves the number of
+// values per lane at each exchange (M*R + 6 - log2(M*R) shuffles instead of
+// 6*M*R), leaving lane groups that each own one output for the epilogue.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace vai_dev {
+
+template <typename T> struct Vec16;
+template <> struct Vec16<half_t> { typedef half8 type; static constexpr int n = 8; };
+template <> struct Vec16<float> { typedef float4v type; static constexpr int n = 4; };
+
+template <int MP, int R, int KCH, typename TI, typename TW>
+__global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
+{
+    typedef typename Vec16<TW>::type wvec;
+    constexpr int EPC = Vec16<TW>::n;      // W elements per 16-byte chunk
+    constexpr int KB = 64 * KCH * EPC;     // K elements per block iteration
+    constexpr int V = MP * R;              // dot products per lane
+    static_assert(V <= 64 && (V & (V - 1)) == 0, "butterfly needs a power of two <= 64");
+    __shared__ TI xs[MP * KB];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t n0 = (blockIdx.x * 4u + wave) * R;
+    const uint32_t K = a.K, N = a.N, M = a.M;
+    const TW* __restrict__ W = (const TW*)a.weight;
+    const TI* __restrict__ X = (const TI*)a.in;
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+
+    for (uint32_t kb = 0; kb < K; kb += KB) {
+        // 1. Every W load of this block for this wave's R rows, issued up front.
+        wvec wv[R][KCH];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int c = 0; c < KCH; ++c) {
+                const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
+                if (n0 + r < N && k < K)
+                    wv[r][c] = __builtin_nontemporal_load((const wvec*)(W + (size_t)(n0 + r) * K + k));
+                else
+                    wv[r][c] = (wvec)0;
+            }
+        // 2. The M input rows of this block into LDS (zero past K and past M).
+        __syncthreads();
+        for (uint32_t i = threadIdx.x * EPC; i < (uint32_t)(MP * KB); i += 256 * EPC) {
+            const uint32_t m = i / KB, kk = kb + (i % KB);
+#pragma unroll
+            for (int e = 0; e < EPC; ++e)
+                xs[i + e] = (m < M && kk + e < K) ? X[(size_t)m * K + kk + e] : (TI)0;
+        }
+        __syncthreads();
+        // 3. Dot products.
+#pragma unroll
+        for (int c = 0; c < KCH; ++c) {
+#pragma unroll
+            for (int m = 0; m < MP; ++m) {
+                float xf[EPC];
+                const TI* xp = xs + m * KB + (c * 64 + lane) * EPC;
+#pragma unroll
+                for (int e = 0; e < EPC; ++e) xf[e] = (float)xp[e];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float s = acc[m * R + r];
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], xf[e], s);
+                    acc[m * R + r] = s;
+                }
+            }
+        }
+    }
+
+    // Butterfly: at offset o a lane keeps the half of its values selected by
+    // (lane & o) and adds the partner's copy of that half.
+    int cnt = V;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        if (cnt > 1) {
+            const int h = cnt / 2;
+            const bool upper = (lane & o) != 0;
+#pragma unroll
+            for (int i = 0; i < h; ++i) {
+                const float send = upper ? acc[i] : acc[i + h];
+                const float keep = upper ? acc[i + h] : acc[i];
+                acc[i] = keep + __shfl_xor(send, o, 64);
+            }
+            cnt = h;
+        } else {
+            acc[0] += __shfl_xor(acc[0], o, 64);
+        }
+    }
+    // Which value this lane now holds, and whether it is the writer of its group.
+    int idx = 0, half = V, low = 64;
+#pragma unroll
+    for (int o = 32; o >= 1 && half > 1; o >>= 1) {
+        half >>= 1;
+        if (lane & o) idx += half;
+        low = o;
+    }
+    if (V == 1) low = 64;
+    if ((lane & (low - 1)) != 0) return;
+    const uint32_t m = idx / R, r = idx % R;
+    if (m >= M || n0 + r >= N) return;
+    const size_t o = (size_t)m * N + n0 + r;
+    const float b = a.bias ? ld(a.bias, a.b_dtype, a.bias_repeat ? o % a.bias_repeat : o) : 0.f;
+    const float rr = a.residual ? ld(a.residual, a.o_dtype, a.residual_repeat ? o % a.residual_repeat : o) : 0.f;
+    st(a.out, a.o_dtype, o, finish(acc[0] + b, rr, a.epilogue, a.residual_order, a.scalar_scale));
+}
+
+// Any K, any alignment: one wave per output column, scalar loads.
+template <int MP>
+__global__ __launch_bounds__(256) void slab_scalar_kernel(SlabParams a)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t n = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (n >= a.N) return;
+    float acc[MP];
+#pragma unroll
+    for (int m = 0; m < MP; ++m) acc[m] = 0.f;
+    for (uint32_t k = lane; k < a.K; k += 64) {
+        const float w = ld(a.weight, a.w_dtype, (size_t)n * a.K + k);
+#pragma unroll
+        for (int m = 0; m < MP; ++m)
+            if ((uint32_t)m < a.M) acc[m] = fmaf(ld(a.in, a.i_dtype, (size_t)m * a.K + k), w, acc[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < MP; ++m) {
+        const float v = wave_sum(acc[m]);
+        if (lane == 0 && (uint32_t)m < a.M) {
+            const size_t o = (size_t)m * a.N + n;
+            const float b = a.bias ? ld(a.bias, a.b_dtype, a.bias_repeat ? o % a.bias_repeat : o) : 0.f;
+            const float rr = a.residual ? ld(a.residual, a.o_dtype, a.residual_repeat ? o % a.residual_repeat : o) : 0.f;
+            st(a.out, a.o_dtype, o, finish(v + b, rr, a.epilogue, a.residual_order, a.scalar_scale));
+        }
+    }
+}
+
+template <int MP, typename TI, typename TW>
+static hipError_t launch_vec(const SlabParams& a, hipStream_t s)
+{
+    // R rows per wave: 4 keeps 16 loads of 16 B in flight per lane at KCH 4.
+    constexpr int R = 4, KCH = 4;
+    const uint32_t blocks = (a.N + 4 * R - 1) / (4 * R);
+    hipLaunchKernelGGL((slab_vec_kernel<MP, R, KCH, TI, TW>), dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int MP>
+static hipError_t launch_m(const SlabParams& a, hipStream_t s)
+{
+    if (a.i_dtype == DT_F16 && a.w_dtype == DT_F16) return launch_vec<MP, half_t, half_t>(a, s);
+    if (a.i_dtype == DT_F32 && a.w_dtype == DT_F16) return launch_vec<MP, float, half_t>(a, s);
+    if (a.i_dtype == DT_F16 && a.w_dtype == DT_F32) return launch_vec<MP, half_t, float>(a, s);
+    return launch_vec<MP, float, float>(a, s);
+}
+
+bool slab_vec_ok(const SlabParams& a)
+{
+    const uint32_t epc = a.w_dtype == DT_F16 ? 8 : 4;
+    const size_t ib = a.i_dtype == DT_F16 ? 2 : 4;
+    return a.K % epc == 0 && ((uintptr_t)a.weight % 16) == 0 && ((uintptr_t)a.in % ib) == 0;
+}
+
+hipError_t slab_launch(const SlabParams& a, hipStream_t s)
+{
+    if (slab_vec_ok(a)) {
+        switch (a.M) {
+        case 1: return launch_m<1>(a, s);
+        case 2: return launch_m<2>(a, s);
+        case 3: case 4: return launch_m<4>(a, s);
+        default: return launch_m<8>(a, s);
+        }
+    }
+    const uint32_t blocks = (a.N + 3) / 4;
+    switch (a.M) {
+    case 1: hipLaunchKernelGGL((slab_scalar_kernel<1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((slab_scalar_kernel<2>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 3: case 4: hipLaunchKernelGGL((slab_scalar_kernel<4>), dim3(blocks), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((slab_scalar_kernel<8>), dim3(blocks), dim3(256), 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
+}   // namespace vai_dev

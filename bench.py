@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of vAi's matmul hot path on one MI355X (BASELINE.json's metric).
+
+A "step" is one pass of the hot path over one batch of synthetic input: one
+launch of the configuration's kernel(s) through the C ABI. K steps are
+captured into one HIP graph (the replay form of the reference's recorded
+command buffer) and timed with HIP events on the stream they run on, with
+inputs already resident in HBM. Bandwidth-bound configurations rotate through
+enough copies of their streamed operand (>= 384 MB) that the 256 MB Infinity
+Cache cannot hold them between launches.
+
+`value` is configs[1] of BASELINE.json -- the Llama-3.2-1B decode GEMV at
+M=1, in HBM GB/s; the prefill GEMM TFLOP/s (config 3) and the other configs
+are reported under "configs" with their own rooflines.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Linear GEMM TFLOP/s (% MFMA peak) + decode GEMV HBM GB/s (% peak)"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+ROTATE_BYTES = 384 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline leg")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--repeats", type=int, default=3)
+    return ap.parse_args()
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+class Case:
+    """One configuration: device buffers, one step's launches, its work."""
+
+    def __init__(self, name, unit, work, bound, peak, launch_fn, kernel, flops, bytes_, dtype):
+        self.name, self.unit, self.work, self.bound, self.peak = name, unit, work, bound, peak
+        self.launch = launch_fn      # launch(step_index) -> None, on the bench stream
+        self.kernel, self.flops, self.bytes, self.dtype = kernel, flops, bytes_, dtype
+
+
+def build_cases(capi, stream, which):
+    import ctypes
+    lib = capi.lib()
+    D = capi.DeviceArray.from_numpy
+    rng = np.random.default_rng(0)
+    cases = {}
+
+    def linear_case(x, ws, bias=None, epi="NONE", gated=False, odt=np.float32):
+        N = ws[0].shape[0] // 2 if gated else ws[0].shape[0]
+        out = capi.DeviceArray(x.shape[:-1] + (N,), odt)
+        args = [capi.linear_args(out, x, w, bias, epi=epi, gated=gated, gate_epi="SILU") for w in ws]
+        need = capi.linear_workspace_size(args[0])
+        keep = [out, x, ws, bias]
+        if need:
+            wsp = capi.DeviceArray((need,), np.uint8)
+            keep.append(wsp)
+            for a in args:
+                a.workspace, a.workspace_bytes = wsp.ptr, wsp.nbytes
+        refs = [ctypes.byref(a) for a in args]
+
+        def launch(i):
+            capi.check(lib.vai_linear_launch(refs[i % len(refs)], stream.ptr), "linear")
+        launch.keep = keep + args
+        return launch, capi.linear_plan(args[0])[0]
+
+    if "1" in which:   # GPT-2 small c_fc, fp32
+        w = (rng.standard_normal((768, 3072)).astype(np.float32) * np.float32(0.02)).T.copy()
+        b = rng.standard_normal(3072).astype(np.float32) * np.float32(0.02)
+        x = rng.standard_normal((128, 768)).astype(np.float32)
+        fn, kern = linear_case(D(x), [D(w)], D(b), epi="GELU_TANH")
+        flops = 2 * 128 * 768 * 3072
+        cases["1"] = Case("GPT-2 c_fc Linear fp32 X[128,768] W[3072,768] +bias GELU-tanh", "TFLOP/s",
+                          flops / 1e12, "mfma", FP32_PEAK_TFLOPS, fn, kern, flops, 11415552, "f32")
+
+    if "2" in which:   # decode GEMV, M in {1,4,8}; rotate W copies past the MALL
+        w0 = f16(rng.standard_normal((2048, 8192)) * 0.02).T.copy()
+        copies = max(2, ROTATE_BYTES // w0.nbytes)
+        ws = [D(w0) for _ in range(copies)]
+        for m in (1, 4, 8):
+            x = D(f16(np.random.default_rng(m).standard_normal((m, 2048))))
+            fn, kern = linear_case(x, ws)
+            byts = 2048 * 8192 * 2 + m * 2048 * 2 + m * 8192 * 4
+            cases[f"2/M={m}"] = Case(f"decode GEMV M={m} K=2048 N=8192 fp16 W, fp32 acc/out", "GB/s",
+                                     byts / 1e9, "hbm", HBM_PEAK_GBS, fn, kern, 2 * m * 2048 * 8192, byts, "f16")
+
+    if "3" in which:   # prefill gate/up, fused SiLU(g)*u
+        wg = f16(rng.standard_normal((3072, 8192)) * 0.02).T
+        wu = f16(rng.standard_normal((3072, 8192)) * 0.02).T
+        w = np.ascontiguousarray(np.concatenate([wg, wu], 0))
+        x = D(f16(rng.standard_normal((2048, 3072))))
+        fn, kern = linear_case(x, [D(w)], gated=True)
+        flops = 2 * 2048 * 3072 * 16384
+        cases["3"] = Case("prefill gate/up X[2048,3072] W[2x8192,3072] fp16, SiLU(g)*u fused, fp32 out",
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn, kern, flops, 180355072, "f16")
+
+    if "4" in which:   # attention scores; rotate S outputs past the MALL
+        q = D(f16(rng.standard_normal((8, 1024, 256))))
+        k = D(f16(rng.standard_normal((8, 1024, 256))))
+        outs = [capi.DeviceArray((8, 1024, 1024), np.float32) for _ in range(ROTATE_BYTES // (8 << 22) + 1)]
+        args = [capi.attn_scores_args(o, q, k, scale=1.0 / 16, causal=True) for o in outs]
+        refs = [ctypes.byref(a) for a in args]
+
+        def fn4(i):
+            capi.check(lib.vai_attn_scores_launch(refs[i % len(refs)], stream.ptr), "scores")
+        fn4.keep = [q, k, outs, args]
+        cases["4"] = Case("attention scores Q,K[8,1024,256] fp16, S=QK^T/16 fp32 causal", "GB/s",
+                          41943040 / 1e9, "hbm", HBM_PEAK_GBS, fn4, "gemm_scores", 2 * 8 * 1024 * 1024 * 256,
+                          41943040, "f16")
+
+    if "5" in which:   # YOLOX 3x3 conv, bias + SiLU
+        wt = D(f16(rng.standard_normal((128, 128, 3, 3)) * 0.03))
+        bias = D(f16(rng.standard_normal(128) * 0.02))
+        x = D(f16(rng.uniform(-1, 1, (1, 128, 80, 80))))
+        out = capi.DeviceArray((1, 128, 80, 80), np.float32)
+        a5 = capi.conv2d_args(out, x, wt, bias, epi="SILU")
+        r5 = ctypes.byref(a5)
+
+        def fn5(i):
+            capi.check(lib.vai_conv2d_launch(r5, stream.ptr), "conv")
+        fn5.keep = [wt, bias, x, out, a5]
+        flops = 2 * 6400 * 128 * 1152
+        cases["5"] = Case("YOLOX-s 3x3 conv in[1,128,80,80] W[128,128,3,3] fp16 +bias SiLU, fp32 out",
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn5, "gemm_conv", flops, 5210368, "f16")
+    return cases
+
+
+def time_case(capi, stream, case, steps, warmup, repeats):
+    for i in range(warmup):
+        case.launch(i)
+    stream.synchronize()
+    graph = capi.Graph(stream, lambda: [case.launch(i) for i in range(steps)])
+    graph.launch()
+    stream.synchronize()
+    t0, t1 = capi.Event(), capi.Event()
+    per_step = []
+    for _ in range(repeats):
+        t0.record(stream.ptr)
+        graph.launch()
+        t1.record(stream.ptr)
+        t1.synchronize()
+        per_step.append(t0.elapsed_ms(t1) / steps)
+    return float(np.median(per_step))
+
+
+def cpu_baseline(budget_s):
+    """The oracle's fp32 GEMV (the linear-slab contract) on the host, timed
+    on a bounded sample of config 2 (M=1): repeated full GEMVs for ~budget_s."""
+    from oracle import oracle
+    rng = np.random.default_rng(0)
+    w = f16(rng.standard_normal((8192, 2048)) * 0.02).astype(np.float32)
+    x = f16(rng.standard_normal((1, 2048))).astype(np.float32)
+    oracle.gemm_f32(x, w)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        oracle.gemm_f32(x, w)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    byts = 2048 * 8192 * 2 + 2048 * 2 + 8192 * 4
+    return {"value": round(byts / dt / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"oracle fp32 GEMV (vai_oracle.c orc_gemm_f32) on config 2 M=1, W widened to fp32; "
+                      f"{n} calls in {budget_s:.0f}s, bytes counted as the fp16 problem's"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding of this path is design-only)"}))
+        sys.exit(2)
+    from vai_amd import _capi as capi
+    capi.check(capi.lib().vai_set_device(0), "set_device")
+    stream = capi.Stream()
+    cases = build_cases(capi, stream, set(args.configs.split(",")))
+    report = {}
+    for key, case in cases.items():
+        ms = time_case(capi, stream, case, args.steps, args.warmup, args.repeats)
+        rate = case.work / (ms * 1e-3)
+        achieved = (case.bytes / 1e9 if case.bound == "hbm" else case.flops / 1e12) / (ms * 1e-3)
+        report[key] = {
+            "workload": case.name, "kernel": case.kernel, "value": round(rate, 3), "unit": case.unit,
+            "ms_per_step": round(ms, 6), "dtype": case.dtype,
+            "roofline": {"bound": case.bound, "achieved": round(achieved, 3), "peak": case.peak,
+                         "unit": "GB/s" if case.bound == "hbm" else "TFLOP/s",
+                         "frac": round(achieved / case.peak, 4), "traffic": None},
+        }
+        print(f"# cfg {key}: {case.name}: {ms*1e3:.2f} us/step, {rate:.1f} {case.unit}, "
+              f"{100*achieved/case.peak:.1f}% of {case.bound} peak [{case.kernel}]", file=sys.stderr, flush=True)
+    prim = report.get("2/M=1") or next(iter(report.values()))
+    line = {
+        "metric": METRIC, "value": prim["value"], "unit": prim["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": prim["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": prim["dtype"], "data": "synthetic",
+        "config": {"workload": prim["workload"], "kernel": prim["kernel"]},
+        "roofline": prim["roofline"],
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
+        "configs": report,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -175,6 +175,17 @@ vai_status vai_event_record(vai_event_t ev, vai_stream_t stream);
 vai_status vai_event_sync(vai_event_t ev);
 vai_status vai_event_elapsed_ms(float* ms, vai_event_t start, vai_event_t stop);
 
+/* Record once, replay: the launches a stream sees between begin and end are
+ * captured into a HIP graph and replayed by vai_graph_launch. This is the
+ * gfx950 form of NeuralNet's command buffer that is recorded once and
+ * resubmitted while shapes stay the same (/root/reference/vai/engine/
+ * neural-net.h:377-449). The stream must not be the null stream. */
+typedef struct vai_graph_s* vai_graph_t;
+vai_status vai_graph_begin_capture(vai_stream_t stream);
+vai_status vai_graph_end_capture(vai_stream_t stream, vai_graph_t* graph);
+vai_status vai_graph_launch(vai_graph_t graph, vai_stream_t stream);
+vai_status vai_graph_destroy(vai_graph_t graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -168,3 +168,31 @@ def test_config3_prefill_gate_up(gpu):
     rows[:2] = [0, 2047]
     want = oracle.gated_mul(oracle.linear(x[rows], w, stage="tile"), epi="SILU")
     assert_close(got[rows], want, TRANS)
+
+
+@pytest.mark.parametrize("m, k, n, gated, odt, epi, residual", [
+    (1024, 512, 8192, False, np.float32, "GELU_TANH", True),     # 256x256 tiles, residual [N]
+    (1000, 320, 8200, False, np.float16, "RELU", False),         # M and N tails
+    (777, 256, 2 * 4160, True, np.float32, "SILU", False),       # gated, M and H tails
+    (2048, 512, 2 * 4096, True, np.float16, "GELU", False),
+])
+def test_linear_big_tile(gpu, m, k, n, gated, odt, epi, residual):
+    """The 256x256 MFMA path (large M, K % 32 == 0) vs the oracle on sampled rows."""
+    rng = np.random.default_rng(0)
+    w = draw(normal((n, k), 0.05), rng, np.float16)
+    b = draw(normal((n,), 0.05), rng, np.float16)
+    x = draw((m, k), rng, np.float16)
+    r = draw((n,), rng, odt) if residual else None
+    kw = dict(gated=True, gate_epi=epi) if gated else dict(epi=epi)
+    a = gpu.linear_args(gpu.DeviceArray((m, n // 2 if gated else n), odt), gpu.DeviceArray((m, k), np.float16),
+                        gpu.DeviceArray((n, k), np.float16), **kw)
+    assert gpu.linear_plan(a)[0].startswith("tile_f16_256x256")
+    got = run_linear(gpu, x, w, b, r, out_dtype=odt, **kw)
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(m - 4, m),
+                                     np.random.default_rng(1).choice(m, 24, replace=False)]))
+    if gated:
+        want = oracle.gated_mul(oracle.linear(x[rows], w, b, stage="tile"), epi=epi, out_dtype=odt)
+    else:
+        want = oracle.linear(x[rows], w, b, r, epi=epi, out_dtype=odt, stage="tile")
+    tol = FP16 if odt == np.float16 else TRANS
+    assert_close(got[rows].astype(np.float32), want.astype(np.float32), tol)

@@ -24,6 +24,7 @@ EXPORTS = [
     "vai_memcpy_d2d", "vai_memset", "vai_stream_create", "vai_stream_destroy", "vai_stream_sync",
     "vai_device_sync", "vai_status_string", "vai_event_create", "vai_event_destroy", "vai_event_record",
     "vai_event_sync", "vai_event_elapsed_ms",
+    "vai_graph_begin_capture", "vai_graph_end_capture", "vai_graph_launch", "vai_graph_destroy",
 ]
 
 
@@ -102,6 +103,10 @@ def lib():
         L.vai_event_record.argtypes = [vp, vp]
         L.vai_event_sync.argtypes = [vp]
         L.vai_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        L.vai_graph_begin_capture.argtypes = [vp]
+        L.vai_graph_end_capture.argtypes = [vp, ctypes.POINTER(vp)]
+        L.vai_graph_launch.argtypes = [vp, vp]
+        L.vai_graph_destroy.argtypes = [vp]
         _lib = L
     return _lib
 
@@ -302,3 +307,43 @@ def device_count():
     n = ctypes.c_int(0)
     st = lib().vai_device_count(ctypes.byref(n))
     return n.value if st == 0 else 0
+
+
+class Stream:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib().vai_stream_create(ctypes.byref(p)), "stream_create")
+        self.ptr = p.value
+
+    def synchronize(self):
+        check(lib().vai_stream_sync(self.ptr), "stream_sync")
+
+    def __del__(self):
+        try:
+            lib().vai_stream_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Captures whatever fn() launches on `stream` into a replayable HIP graph."""
+
+    def __init__(self, stream, fn):
+        self.stream = stream
+        check(lib().vai_graph_begin_capture(stream.ptr), "begin_capture")
+        try:
+            fn()
+        finally:
+            g = ctypes.c_void_p()
+            st = lib().vai_graph_end_capture(stream.ptr, ctypes.byref(g))
+        check(st, "end_capture")
+        self.ptr = g.value
+
+    def launch(self):
+        check(lib().vai_graph_launch(self.ptr, self.stream.ptr), "graph_launch")
+
+    def __del__(self):
+        try:
+            lib().vai_graph_destroy(self.ptr)
+        except Exception:
+            pass

@@ -26,7 +26,7 @@ size_t dtype_bytes(int32_t d) { return d == VAI_DTYPE_F16 ? 2 : 4; }
 vai_status hip_status(hipError_t e) { return e == hipSuccess ? VAI_OK : (vai_status)e; }
 
 struct LinearPlan {
-    enum Kind { Slab, SlabThenGate, Tile } kind;
+    enum Kind { Slab, SlabThenGate, Tile, BigTile } kind;
     GemmTile tile;
     uint32_t bm, bn;
     uint32_t split_size, splits;
@@ -70,6 +70,18 @@ LinearPlan plan_linear(const vai_linear_args* a)
         return p;
     }
     p.kind = LinearPlan::Tile;
+    {
+        GemmParams g{};
+        g.a_dtype = a->i_dtype; g.b_dtype = a->w_dtype; g.M = M; g.N = N; g.K = K; g.H = a->gated ? N / 2 : 0;
+        g.A = a->in; g.B = a->weight; g.splits = 1; g.batch = 1;
+        if (a->split_size == 0 && gemm_big_ok(g, a->gated)) {
+            p.kind = LinearPlan::BigTile;
+            p.splits = 1;
+            p.split_size = K;
+            p.workspace = 0;
+            return p;
+        }
+    }
     const bool f32 = a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32;
     const uint32_t bk = f32 ? 16 : 32;
     // Candidate tiles, largest first (the gated kernel pairs fragments, so its
@@ -131,11 +143,13 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
     if (st != VAI_OK) return st;
     const LinearPlan p = plan_linear(a);
     char buf[64];
-    if (p.kind != LinearPlan::Tile) {
+    if (p.kind == LinearPlan::Slab || p.kind == LinearPlan::SlabThenGate) {
         SlabParams sp{};
         sp.K = a->K; sp.w_dtype = a->w_dtype; sp.i_dtype = a->i_dtype; sp.weight = a->weight; sp.in = a->in;
         snprintf(buf, sizeof buf, "%s%s", slab_vec_ok(sp) ? "slab" : "slab_scalar",
                  p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
+    } else if (p.kind == LinearPlan::BigTile) {
+        snprintf(buf, sizeof buf, "tile_f16_256x256%s", a->gated ? "_gated" : "");
     } else {
         const bool f32 = a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32;
         snprintf(buf, sizeof buf, "tile_%s_%s%s", f32 ? "f32" : "f16", tile_name(p.tile, a->gated),
@@ -154,7 +168,7 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
     const LinearPlan p = plan_linear(a);
     if (p.workspace && (!a->workspace || a->workspace_bytes < p.workspace)) return VAI_ERR_WORKSPACE;
 
-    if (p.kind != LinearPlan::Tile) {
+    if (p.kind == LinearPlan::Slab || p.kind == LinearPlan::SlabThenGate) {
         SlabParams sp{};
         sp.in = a->in; sp.weight = a->weight; sp.bias = a->bias; sp.residual = a->residual;
         sp.M = a->M; sp.N = a->N; sp.K = a->K;
@@ -187,6 +201,7 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
     g.H = a->gated ? a->N / 2 : 0;
     if (p.splits > 1) { g.C = a->workspace; g.c_dtype = VAI_DTYPE_F32; }
     else { g.C = a->out; g.c_dtype = a->o_dtype; }
+    if (p.kind == LinearPlan::BigTile) return hip_status(gemm_big_launch(g, a->gated != 0, s));
     hipError_t e = gemm_launch(g, a->gated ? BKind::Gated : BKind::Dense,
                                a->gated ? EpiKind::Gated : EpiKind::Linear, p.tile, s);
     if (e != hipSuccess || p.splits == 1) return hip_status(e);
@@ -297,6 +312,45 @@ vai_status vai_event_sync(vai_event_t ev) { return hip_status(hipEventSynchroniz
 vai_status vai_event_elapsed_ms(float* ms, vai_event_t a, vai_event_t b)
 {
     return hip_status(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+}
+
+struct vai_graph_s {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+vai_status vai_graph_begin_capture(vai_stream_t s)
+{
+    if (!s) return VAI_ERR_INVALID_ARG;
+    return hip_status(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal));
+}
+
+vai_status vai_graph_end_capture(vai_stream_t s, vai_graph_t* out)
+{
+    if (!s || !out) return VAI_ERR_INVALID_ARG;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)s, &g);
+    if (e != hipSuccess) return hip_status(e);
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) { hipGraphDestroy(g); return hip_status(e); }
+    *out = new vai_graph_s{g, x};
+    return VAI_OK;
+}
+
+vai_status vai_graph_launch(vai_graph_t g, vai_stream_t s)
+{
+    if (!g) return VAI_ERR_INVALID_ARG;
+    return hip_status(hipGraphLaunch(g->exec, (hipStream_t)s));
+}
+
+vai_status vai_graph_destroy(vai_graph_t g)
+{
+    if (!g) return VAI_OK;
+    hipGraphExecDestroy(g->exec);
+    hipGraphDestroy(g->graph);
+    delete g;
+    return VAI_OK;
 }
 
 const char* vai_status_string(vai_status s)

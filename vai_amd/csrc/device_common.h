@@ -3,7 +3,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace vai_dev {
+
+// Calls f(std::integral_constant<int, I>{}) for I = 0..N-1, fully unrolled at
+// compile time (register arrays indexed by I stay registers).
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
+        (f(std::integral_constant<int, I>{}), ...);
+    }(std::make_integer_sequence<int, N>{});
+}
 
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));

@@ -72,6 +72,10 @@ enum class GemmTile : int { T64x64 = 0, T128x64 = 1, T128x128 = 2, T256x128 = 3 
 
 hipError_t gemm_launch(const GemmParams& p, BKind bk, EpiKind ek, GemmTile tile, hipStream_t s);
 
+// The 256x256x64 fp16 MFMA GEMM for large, K%64 == 0 shapes (Linear / gated).
+bool gemm_big_ok(const GemmParams& p, bool gated);
+hipError_t gemm_big_launch(const GemmParams& p, bool gated, hipStream_t s);
+
 // Split-K fold for Linear: O = s*epi(sum_z P[z] + B) (+R).
 hipError_t linear_reduce_launch(void* out, int o_dtype, const float* partials, uint32_t splits, size_t MN,
                                 const void* bias, int b_dtype, uint32_t bias_repeat,

@@ -21,6 +21,55 @@ template <typename T> struct Vec16;
 template <> struct Vec16<half_t> { typedef half8 type; static constexpr int n = 8; };
 template <> struct Vec16<float> { typedef float4v type; static constexpr int n = 4; };
 
+// Butterfly over a wave of CNT values per lane: at offset O a lane keeps the
+// half selected by (lane & O) and adds its partner's copy of that half, so
+// each exchange halves the values per lane; once one is left, plain xor-adds.
+template <int CNT, int O>
+__device__ __forceinline__ void butterfly(float* acc, int lane)
+{
+    if constexpr (O >= 1) {
+        if constexpr (CNT > 1) {
+            constexpr int H = CNT / 2;
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float send = upper ? acc[i] : acc[i + H];
+                const float keep = upper ? acc[i + H] : acc[i];
+                acc[i] = keep + __shfl_xor(send, O, 64);
+            }
+            butterfly<H, O / 2>(acc, lane);
+        } else {
+            acc[0] += __shfl_xor(acc[0], O, 64);
+            butterfly<1, O / 2>(acc, lane);
+        }
+    }
+}
+
+// The value index a lane holds after butterfly<V, 32>.
+template <int V>
+__device__ __forceinline__ int butterfly_index(int lane)
+{
+    int idx = 0, h = V;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        if (h > 1) {
+            h >>= 1;
+            if (lane & o) idx += h;
+        }
+    }
+    return idx;
+}
+
+// Lanes that agree on their value form groups of this size; the group's
+// lowest lane writes.
+template <int V>
+constexpr int butterfly_low()
+{
+    int h = V, low = 64;
+    for (int o = 32; o >= 1 && h > 1; o >>= 1) { h >>= 1; low = o; }
+    return low;
+}
+
 template <int MP, int R, int KCH, typename TI, typename TW>
 __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
 {
@@ -59,9 +108,10 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
         __syncthreads();
         for (uint32_t i = threadIdx.x * EPC; i < (uint32_t)(MP * KB); i += 256 * EPC) {
             const uint32_t m = i / KB, kk = kb + (i % KB);
-#pragma unroll
-            for (int e = 0; e < EPC; ++e)
-                xs[i + e] = (m < M && kk + e < K) ? X[(size_t)m * K + kk + e] : (TI)0;
+            // EPC elements of X per thread: K % EPC == 0 keeps them in one row.
+            typedef TI xvec __attribute__((ext_vector_type(EPC)));
+            xvec v = (m < M && kk < K) ? *(const xvec*)(X + (size_t)m * K + kk) : (xvec)0;
+            *(xvec*)(xs + i) = v;
         }
         __syncthreads();
         // 3. Dot products.
@@ -84,35 +134,10 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
         }
     }
 
-    // Butterfly: at offset o a lane keeps the half of its values selected by
-    // (lane & o) and adds the partner's copy of that half.
-    int cnt = V;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        if (cnt > 1) {
-            const int h = cnt / 2;
-            const bool upper = (lane & o) != 0;
-#pragma unroll
-            for (int i = 0; i < h; ++i) {
-                const float send = upper ? acc[i] : acc[i + h];
-                const float keep = upper ? acc[i + h] : acc[i];
-                acc[i] = keep + __shfl_xor(send, o, 64);
-            }
-            cnt = h;
-        } else {
-            acc[0] += __shfl_xor(acc[0], o, 64);
-        }
-    }
-    // Which value this lane now holds, and whether it is the writer of its group.
-    int idx = 0, half = V, low = 64;
-#pragma unroll
-    for (int o = 32; o >= 1 && half > 1; o >>= 1) {
-        half >>= 1;
-        if (lane & o) idx += half;
-        low = o;
-    }
-    if (V == 1) low = 64;
-    if ((lane & (low - 1)) != 0) return;
+    // Butterfly over the wave; afterwards lane `lane` holds value idx.
+    butterfly<V, 32>(acc, lane);
+    const int idx = butterfly_index<V>(lane);
+    if ((lane & (butterfly_low<V>() - 1)) != 0) return;
     const uint32_t m = idx / R, r = idx % R;
     if (m >= M || n0 + r >= N) return;
     const size_t o = (size_t)m * N + n0 + r;
@@ -172,7 +197,7 @@ bool slab_vec_ok(const SlabParams& a)
 {
     const uint32_t epc = a.w_dtype == DT_F16 ? 8 : 4;
     const size_t ib = a.i_dtype == DT_F16 ? 2 : 4;
-    return a.K % epc == 0 && ((uintptr_t)a.weight % 16) == 0 && ((uintptr_t)a.in % ib) == 0;
+    return a.K % epc == 0 && ((uintptr_t)a.weight % 16) == 0 && ((uintptr_t)a.in % (epc * ib)) == 0;
 }
 
 hipError_t slab_launch(const SlabParams& a, hipStream_t s)

@@ -172,7 +172,7 @@ def test_config3_prefill_gate_up(gpu):
 
 @pytest.mark.parametrize("m, k, n, gated, odt, epi, residual", [
     (1024, 512, 8192, False, np.float32, "GELU_TANH", True),     # 256x256 tiles, residual [N]
-    (1000, 320, 8200, False, np.float16, "RELU", False),         # M and N tails
+    (1000, 384, 8200, False, np.float16, "RELU", False),         # M and N tails
     (777, 256, 2 * 4160, True, np.float32, "SILU", False),       # gated, M and H tails
     (2048, 512, 2 * 4096, True, np.float16, "GELU", False),
 ])

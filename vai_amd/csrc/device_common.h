@@ -37,14 +37,27 @@ __device__ __forceinline__ void st(void* p, int dt, size_t i, float v)
 
 // Epilogues of vai::Epilogue, as the reference's activation.h states them
 // (/root/reference/vai/shaders/common/activation.h:19-58): GELU (erf) through
-// Abramowitz-Stegun 7.1.26, GELU-tanh, SiLU, sigmoid.
+// Abramowitz-Stegun 7.1.26, GELU-tanh, SiLU, sigmoid. exp and reciprocal use
+// the hardware v_exp_f32 / v_rcp_f32 (about 1 ulp each): the reference's own
+// tier for these is 1e-4 relative, and IEEE exp + division made the GEMM
+// epilogue VALU-bound. tanh(y) = 1 - 2 / (e^{2y} + 1) saturates to +-1 for
+// large |y| (e^{2y} = inf gives 1 - 0) and keeps an absolute error of a few
+// ulp of 1 near 0.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
 __device__ __forceinline__ float erf_as(float x)
 {
-    const float t = 1.0f / (1.0f + 0.3275911f * fabsf(x));
+    const float t = fast_rcp(1.0f + 0.3275911f * fabsf(x));
     const float p = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t
                      + 0.254829592f) * t;
     const float s = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
-    return s * (1.0f - p * expf(-x * x));
+    return s * (1.0f - p * fast_exp(-x * x));
+}
+
+__device__ __forceinline__ float fast_tanh(float y)
+{
+    return 1.0f - 2.0f * fast_rcp(fast_exp(2.0f * y) + 1.0f);
 }
 
 __device__ __forceinline__ float epilogue(float x, uint32_t epi)
@@ -52,9 +65,9 @@ __device__ __forceinline__ float epilogue(float x, uint32_t epi)
     switch (epi) {
     case 1: return x > 0.f ? x : 0.f;
     case 2: return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
-    case 3: return 0.5f * x * (1.0f + tanhf(0.79788456080286535f * (x + 0.044715f * x * x * x)));
-    case 4: return x / (1.0f + expf(-x));
-    case 5: return 1.0f / (1.0f + expf(-x));
+    case 3: return 0.5f * x * (1.0f + fast_tanh(0.79788456080286535f * (x + 0.044715f * x * x * x)));
+    case 4: return x * fast_rcp(1.0f + fast_exp(-x));
+    case 5: return fast_rcp(1.0f + fast_exp(-x));
     default: return x;
     }
 }

@@ -109,6 +109,12 @@ vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int3
  * weights (Convolution::validateInputs, /root/reference/vai/nodes/
  * convolution.h:4137-4160). Replaces runK3S1Implicit / the implicit-GEMM
  * plan (/root/reference/vai/nodes/convolution.h:6237-6283, 6616-6644).
+ * With fp16 weights the kernel reads them packed [tap][co][ci] (channels
+ * padded to a multiple of 32): pass a buffer that vai_conv2d_pack_weight()
+ * filled once as packed_weight (the reference transforms conv weights once,
+ * /root/reference/vai/nodes/convolution.h:6224-6235), or leave it NULL and
+ * pass a workspace of vai_conv2d_workspace_size() bytes in which every call
+ * packs them first.
  * ------------------------------------------------------------------------- */
 typedef struct {
     void* out;
@@ -121,9 +127,18 @@ typedef struct {
     int32_t o_dtype, i_dtype, w_dtype;
     uint32_t epilogue;
     uint32_t residual_order;
+    void* workspace;
+    size_t workspace_bytes;
+    const void* packed_weight;   /* NULL, or vai_conv2d_pack_weight()'s output */
 } vai_conv2d_args;
 
 vai_status vai_conv2d_launch(const vai_conv2d_args* args, vai_stream_t stream);
+size_t vai_conv2d_workspace_size(const vai_conv2d_args* args);
+/* Size of, and the one-time fill of, the packed weight for args (0 / no-op
+ * when args take the fp32 path, which reads the weight as given). */
+size_t vai_conv2d_packed_weight_size(const vai_conv2d_args* args);
+vai_status vai_conv2d_pack_weight(const vai_conv2d_args* args, void* packed, size_t packed_bytes,
+                                  vai_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Attention scores: S[b,h,i,j] = scale * sum_d Q[b,h,i,d] K[b,h/g,j,d],

@@ -116,3 +116,28 @@ def test_config4_attention_scores(gpu):
     for h in (0, 7):
         want = oracle.attn_scores(q[h:h + 1], k[h:h + 1], scale=1.0 / 16, causal=True)
         assert_close(got[h:h + 1], want, FP32)
+
+
+@pytest.mark.parametrize("ci, co, ks, stride, hw, dt_in", [(40, 48, 3, 1, 19, np.float16), (64, 32, 1, 1, 24, np.float32),
+                                                           (16, 24, 3, 2, 21, np.float16), (96, 40, 3, 2, 33, np.float32)])
+def test_conv_packed_weight_reuse(gpu, ci, co, ks, stride, hw, dt_in):
+    """A weight packed once (vai_conv2d_pack_weight) gives the same output as
+    the per-call pack, on two different inputs."""
+    rng = np.random.default_rng(2)
+    w = draw(normal((co, ci, ks, ks), 0.1), rng, np.float16)
+    b = draw(normal((co,), 0.1), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    dw, db = D(w), D(b)
+    ho = (hw - 1) // stride + 1
+    for seed in (0, 1):
+        x = draw((2, ci, hw, hw), np.random.default_rng(seed), dt_in)
+        dx = D(x)
+        o1 = gpu.DeviceArray((2, co, ho, ho), np.float32)
+        gpu.conv2d(o1, dx, dw, db, stride=stride, epi="SILU")
+        a = gpu.conv2d_args(o1, dx, dw, db, stride=stride, epi="SILU")
+        packed = gpu.conv2d_pack_weight(a)
+        assert packed is not None
+        o2 = gpu.DeviceArray((2, co, ho, ho), np.float32)
+        gpu.conv2d(o2, dx, dw, db, stride=stride, epi="SILU", packed=packed)
+        np.testing.assert_array_equal(o1.numpy(), o2.numpy())
+        assert_close(o2.numpy(), oracle.conv2d(x, w, b, stride=stride, epi="SILU"), FP16)

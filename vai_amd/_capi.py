@@ -19,7 +19,8 @@ RESIDUAL_ORDERS = {"AFTER_EPILOGUE": 0, "BEFORE_EPILOGUE": 1}
 # Every symbol include/vai_amd.h declares (checked by tests/test_capi_symbols.py).
 EXPORTS = [
     "vai_linear_launch", "vai_linear_workspace_size", "vai_linear_plan", "vai_gated_mul_launch",
-    "vai_conv2d_launch", "vai_attn_scores_launch",
+    "vai_conv2d_launch", "vai_conv2d_workspace_size", "vai_conv2d_packed_weight_size", "vai_conv2d_pack_weight",
+    "vai_attn_scores_launch",
     "vai_device_count", "vai_set_device", "vai_malloc", "vai_free", "vai_memcpy_h2d", "vai_memcpy_d2h",
     "vai_memcpy_d2d", "vai_memset", "vai_stream_create", "vai_stream_destroy", "vai_stream_sync",
     "vai_device_sync", "vai_status_string", "vai_event_create", "vai_event_destroy", "vai_event_record",
@@ -51,6 +52,8 @@ class Conv2dArgs(ctypes.Structure):
         ("co", ctypes.c_uint32), ("kernel", ctypes.c_uint32), ("stride", ctypes.c_uint32),
         ("o_dtype", ctypes.c_int32), ("i_dtype", ctypes.c_int32), ("w_dtype", ctypes.c_int32),
         ("epilogue", ctypes.c_uint32), ("residual_order", ctypes.c_uint32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("packed_weight", ctypes.c_void_p),
     ]
 
 
@@ -84,6 +87,11 @@ def lib():
         L.vai_linear_plan.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_char_p, sz, ctypes.POINTER(u32)]
         L.vai_gated_mul_launch.argtypes = [vp, i32, vp, i32, u32, u32, u32, vp]
         L.vai_conv2d_launch.argtypes = [ctypes.POINTER(Conv2dArgs), vp]
+        L.vai_conv2d_workspace_size.argtypes = [ctypes.POINTER(Conv2dArgs)]
+        L.vai_conv2d_workspace_size.restype = sz
+        L.vai_conv2d_packed_weight_size.argtypes = [ctypes.POINTER(Conv2dArgs)]
+        L.vai_conv2d_packed_weight_size.restype = sz
+        L.vai_conv2d_pack_weight.argtypes = [ctypes.POINTER(Conv2dArgs), vp, sz, vp]
         L.vai_attn_scores_launch.argtypes = [ctypes.POINTER(AttnScoresArgs), vp]
         L.vai_malloc.argtypes = [ctypes.POINTER(vp), sz]
         L.vai_free.argtypes = [vp]
@@ -249,9 +257,34 @@ def conv2d_args(out, inp, weight, bias=None, scale=None, residual=None, *, strid
     return a
 
 
-def conv2d(out, inp, weight, bias=None, scale=None, residual=None, stream=None, **kw):
+def conv2d_workspace_size(args):
+    return lib().vai_conv2d_workspace_size(ctypes.byref(args))
+
+
+def conv2d_pack_weight(args, stream=None):
+    """Packs args' weight once; returns the packed buffer (or None on the fp32 path)."""
+    n = lib().vai_conv2d_packed_weight_size(ctypes.byref(args))
+    if not n:
+        return None
+    packed = DeviceArray((n,), np.uint8)
+    check(lib().vai_conv2d_pack_weight(ctypes.byref(args), packed.ptr, packed.nbytes, stream), "pack_weight")
+    return packed
+
+
+def conv2d(out, inp, weight, bias=None, scale=None, residual=None, stream=None, packed=None, **kw):
+    """Launches the convolution; allocates its packing workspace if needed.
+    packed: a conv2d_pack_weight() result to skip the per-call weight pack."""
     a = conv2d_args(out, inp, weight, bias, scale, residual, **kw)
+    if packed is not None:
+        a.packed_weight = packed.ptr
+    ws = None
+    need = conv2d_workspace_size(a)
+    if need:
+        ws = DeviceArray((need,), np.uint8)
+        a.workspace, a.workspace_bytes = ws.ptr, ws.nbytes
     check(lib().vai_conv2d_launch(ctypes.byref(a), stream), "vai_conv2d_launch")
+    if ws is not None:
+        check(lib().vai_stream_sync(stream), "sync")
     return out
 
 

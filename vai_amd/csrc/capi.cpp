@@ -222,7 +222,7 @@ vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int3
     return hip_status(gated_mul_launch(out, o_dtype, in, i_dtype, rows, H, epilogue, (hipStream_t)stream));
 }
 
-vai_status vai_conv2d_launch(const vai_conv2d_args* a, vai_stream_t stream)
+static vai_status check_conv(const vai_conv2d_args* a)
 {
     if (!a || !a->out || !a->in || !a->weight) return VAI_ERR_INVALID_ARG;
     if (!dtype_ok(a->o_dtype) || !dtype_ok(a->i_dtype) || !dtype_ok(a->w_dtype)) return VAI_ERR_DTYPE;
@@ -233,7 +233,61 @@ vai_status vai_conv2d_launch(const vai_conv2d_args* a, vai_stream_t stream)
         return VAI_ERR_SHAPE;
     if (a->kernel == 0 || a->kernel % 2 == 0) return VAI_ERR_SHAPE;
     if (a->epilogue > VAI_EPI_SIGMOID || a->residual_order > 1) return VAI_ERR_INVALID_ARG;
+    return VAI_OK;
+}
+
+// fp16 weights and a band that fits in LDS take the packed NHWC kernel.
+static bool conv_packed(const vai_conv2d_args* a)
+{
+    const uint32_t wo = (a->wi - 1) / a->stride + 1;
+    return a->w_dtype == VAI_DTYPE_F16 && conv_nhwc_ok(a->ci, a->wi, wo, a->kernel);
+}
+
+size_t vai_conv2d_packed_weight_size(const vai_conv2d_args* a)
+{
+    if (check_conv(a) != VAI_OK || !conv_packed(a)) return 0;
+    return conv_packed_weight_bytes(a->ci, a->co, a->kernel);
+}
+
+size_t vai_conv2d_workspace_size(const vai_conv2d_args* a)
+{
+    if (a && a->packed_weight) return 0;
+    return vai_conv2d_packed_weight_size(a);
+}
+
+vai_status vai_conv2d_pack_weight(const vai_conv2d_args* a, void* packed, size_t bytes, vai_stream_t stream)
+{
+    const vai_status st = check_conv(a);
+    if (st != VAI_OK) return st;
+    if (!conv_packed(a)) return VAI_OK;
+    if (!packed || bytes < conv_packed_weight_bytes(a->ci, a->co, a->kernel)) return VAI_ERR_WORKSPACE;
+    return hip_status(conv_pack_weight((half_t_storage*)packed, (const half_t_storage*)a->weight, a->ci, a->co,
+                                       a->kernel, (hipStream_t)stream));
+}
+
+vai_status vai_conv2d_launch(const vai_conv2d_args* a, vai_stream_t stream)
+{
+    const vai_status st = check_conv(a);
+    if (st != VAI_OK) return st;
     const uint32_t ho = (a->hi - 1) / a->stride + 1, wo = (a->wi - 1) / a->stride + 1;
+    if (conv_packed(a)) {
+        const void* wp = a->packed_weight;
+        if (!wp) {
+            const size_t need = conv_packed_weight_bytes(a->ci, a->co, a->kernel);
+            if (!a->workspace || a->workspace_bytes < need) return VAI_ERR_WORKSPACE;
+            hipError_t e = conv_pack_weight((half_t_storage*)a->workspace, (const half_t_storage*)a->weight, a->ci,
+                                            a->co, a->kernel, (hipStream_t)stream);
+            if (e != hipSuccess) return hip_status(e);
+            wp = a->workspace;
+        }
+        ConvParams c{};
+        c.out = a->out; c.x = a->in; c.wp = (const half_t_storage*)wp;
+        c.bias = a->bias; c.scale = a->scale; c.residual = a->residual;
+        c.o_dtype = a->o_dtype; c.residual_dtype = a->i_dtype;
+        c.batch = a->batch; c.ci = a->ci; c.hi = a->hi; c.wi = a->wi; c.co = a->co; c.ho = ho; c.wo = wo;
+        c.ks = a->kernel; c.stride = a->stride; c.epilogue = a->epilogue; c.residual_order = a->residual_order;
+        return hip_status(conv_launch(c, a->i_dtype, (hipStream_t)stream));
+    }
     GemmParams g{};
     g.A = a->weight; g.B = a->in; g.C = a->out;
     g.a_dtype = a->w_dtype; g.b_dtype = a->i_dtype; g.c_dtype = a->o_dtype;

@@ -1,0 +1,257 @@
+// conv.hip -- implicit-GEMM convolution for fp16 weights on gfx950 (the role
+// of /root/reference/vai/shaders/conv-k3s1-implicit-gemm.comp and
+// conv-implicit-gemm.comp; plan choice in convolution.h:5408-5443).
+//
+//   out[b,co,ho,wo] = epi(scale[co] * sum_{c,kh,kw} W[co,c,kh,kw] X[b,c,ho*s+kh-p,wo*s+kw-p]
+//                         + bias[co] (+R)) (+R)
+//
+// The reduction index is (tap, channel) here instead of the reference's
+// c*k*k + tap: the order of an fp32 sum is free, and this one makes 8
+// consecutive k values 8 consecutive channels, which is what one MFMA lane
+// consumes. Weights are packed once to that order, [tap][co][c] with channels
+// zero-padded to a multiple of 32 (the reference transforms conv weights once
+// too, convolution.h:6224-6235).
+//
+// Forward kernel: one workgroup of 8 waves per (32 output channels, one
+// output row, image). It stages the k input rows it needs from NCHW into LDS
+// transposed to [row][column][channel], so 8 channels are one 16-byte LDS
+// read; weight fragments come straight from the packed buffer (L2-resident)
+// into VGPRs. Waves = 4 channel blocks x 2 halves of the 32 output channels;
+// each runs v_mfma_f32_16x16x32_f16 over every tap, their partial sums meet
+// in LDS, and scale, bias, residual and the activation are applied once per
+// output with coalesced stores. Only the input band occupies LDS, so two
+// workgroups (16 waves) share a CU and hide each other's latencies.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace vai_dev {
+
+namespace cv {
+constexpr int CO_TILE = 32;
+constexpr int MAX_WO_FRAGS = 8;          // output row <= 128 positions
+inline __host__ __device__ uint32_t ci32(uint32_t ci) { return (ci + 31) / 32 * 32; }
+inline __host__ __device__ uint32_t cip(uint32_t ci) { return ci32(ci) + 8; }   // LDS row stride (halves)
+}
+
+// W [Co, C, k, k] (fp16) -> Wp [k*k][Co][C32] fp16, zero-padded channels.
+// One workgroup per output channel: its C*k*k weights are read contiguously
+// into LDS and written out tap-major.
+__global__ __launch_bounds__(256) void pack_weight_kernel(half_t* __restrict__ dst, const half_t* __restrict__ w,
+                                                          uint32_t Co, uint32_t C, uint32_t C32, uint32_t kk)
+{
+    extern __shared__ half_t row[];
+    const uint32_t co = blockIdx.x;
+    const size_t n = (size_t)C * kk;
+    for (size_t i = threadIdx.x; i < n; i += 256) row[i] = w[(size_t)co * n + i];
+    __syncthreads();
+    for (size_t i = threadIdx.x; i < (size_t)kk * C32; i += 256) {
+        const uint32_t c = i % C32, tap = i / C32;
+        dst[((size_t)tap * Co + co) * C32 + c] = c < C ? row[(size_t)c * kk + tap] : (half_t)0;
+    }
+}
+
+template <int KS, int NF, typename TI>
+__global__ __launch_bounds__(512) void conv_kernel(ConvParams p)
+{
+    using namespace cv;
+    extern __shared__ half8 smem[];
+    const uint32_t C32 = ci32(p.ci), CIP = cip(p.ci);
+    constexpr int PAD = KS / 2;
+    const uint32_t WiP = p.wi + 2 * PAD;
+    half_t* xs = (half_t*)smem;                              // [KS][WiP][CIP]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cw = wave & 3, half = wave >> 2;               // channel-block lane, output-channel half
+    const uint32_t co0 = blockIdx.x * CO_TILE, ho = blockIdx.y, b = blockIdx.z;
+    const int fr = lane & 15, fg = lane >> 4;
+    const uint32_t nblk = C32 / 32;
+
+    // A fragments straight from the packed weight (L2-resident, shared by all
+    // blocks): issued first so their latency hides behind the input staging.
+    half8 wa[KS * KS];
+    const uint32_t co_a = min(co0 + half * 16 + fr, p.co - 1);
+    auto load_w = [&](uint32_t cb) {
+#pragma unroll
+        for (int tap = 0; tap < KS * KS; ++tap)
+            wa[tap] = *(const half8*)(p.wp + ((size_t)tap * p.co + co_a) * C32 + cb * 32 + fg * 8);
+    };
+    if ((uint32_t)cw < nblk) load_w(cw);
+
+    // ---- input rows: NCHW -> LDS [row][pad + w][c] ----
+    // Thread t takes channel c = t % C32 (lanes = consecutive channels, so the
+    // 2-byte LDS writes of a wave land in distinct banks) and every
+    // (512 / C32)-th run of 8 columns.
+    {
+        const uint32_t nwc = (p.wi + 7) / 8;
+        const uint32_t tpc = 512 / C32 ? 512 / C32 : 1;       // threads per channel
+        const uint32_t c = tid % C32, wc0 = tid / C32;
+        const bool active = (uint32_t)tid < tpc * C32 || C32 > 512;
+        const size_t plane = (size_t)p.hi * p.wi;
+        const bool vec = p.wi % 8 == 0 && ((uintptr_t)p.x % (8 * sizeof(TI))) == 0;
+        for (uint32_t cc = c; cc < C32; cc += 512) {
+#pragma unroll
+            for (int r = 0; r < KS; ++r) {
+                const int hi = (int)(ho * p.stride) + r - PAD;
+                const bool row_ok = hi >= 0 && hi < (int)p.hi && cc < p.ci;
+                half_t* dst = xs + ((size_t)r * WiP) * CIP + cc;
+                if (wc0 == 0 && active) {
+#pragma unroll
+                    for (int e = 0; e < PAD; ++e) {
+                        dst[(size_t)e * CIP] = (half_t)0;
+                        dst[(size_t)(PAD + p.wi + e) * CIP] = (half_t)0;
+                    }
+                }
+                if (!active) continue;
+                const TI* src = (const TI*)p.x + ((size_t)b * p.ci + (cc < p.ci ? cc : 0)) * plane +
+                                (size_t)(row_ok ? hi : 0) * p.wi;
+                for (uint32_t wb = wc0; wb < nwc; wb += 4 * tpc) {
+                    float v[4][8];
+                    if (vec) {   // wi % 8 == 0: one 16- (fp16) or 32-byte (fp32) load per run
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t w0 = (wb + u * tpc) * 8;
+                            typedef TI tv8 __attribute__((ext_vector_type(8)));
+                            const tv8 t = (row_ok && w0 < p.wi) ? *(const tv8*)(src + w0) : (tv8)0;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[u][e] = (float)t[e];
+                        }
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t w0 = (wb + u * tpc) * 8;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e)
+                                v[u][e] = (row_ok && w0 + e < p.wi) ? (float)src[w0 + e] : 0.f;
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const uint32_t w0 = (wb + u * tpc) * 8;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (w0 + e < p.wi) dst[(size_t)(PAD + w0 + e) * CIP] = (half_t)v[u][e];
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- MFMAs: 16 output channels x the row, this wave's channel blocks ----
+    constexpr int nf = NF;                                   // output-position fragments (compile time:
+                                                             // a runtime count makes the loop nest spill)
+    float4v acc[MAX_WO_FRAGS];
+#pragma unroll
+    for (int f = 0; f < MAX_WO_FRAGS; ++f) acc[f] = (float4v)0.f;
+    uint32_t wo_s[MAX_WO_FRAGS];
+#pragma unroll
+    for (int f = 0; f < MAX_WO_FRAGS; ++f) wo_s[f] = min((uint32_t)(f * 16 + fr), p.wo - 1) * p.stride;
+    for (uint32_t cb = cw; cb < nblk; cb += 4) {
+        if (cb != (uint32_t)cw) load_w(cb);
+        const uint32_t cofs = cb * 32 + fg * 8;
+#pragma unroll
+        for (int kh = 0; kh < KS; ++kh) {
+#pragma unroll
+            for (int kw = 0; kw < KS; ++kw) {
+                const half_t* xrow = xs + ((size_t)kh * WiP + kw) * CIP + cofs;
+#pragma unroll
+                for (int f = 0; f < MAX_WO_FRAGS; ++f) {
+                    if (f < nf) {
+                        const half8 bv = *(const half8*)(xrow + (size_t)wo_s[f] * CIP);
+                        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[kh * KS + kw], bv, acc[f], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- cross-wave sum in LDS, then the epilogue ----
+    // D[i][j] of a 16x16 fragment sits in lane j + 16*(i/4), register i%4.
+    float* red = (float*)smem;                               // [4 channel lanes][32 co][16*nf positions]
+    const uint32_t rw = (uint32_t)nf * 16;
+#pragma unroll
+    for (int f = 0; f < MAX_WO_FRAGS; ++f)
+        if (f < nf)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[((size_t)cw * CO_TILE + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
+    __syncthreads();
+    const size_t HoWo = (size_t)p.ho * p.wo;
+    for (uint32_t col = tid >> 6; col < (uint32_t)CO_TILE; col += 8) {
+        const uint32_t co = co0 + col;
+        if (co >= p.co) break;
+        const float bias = p.bias ? ld(p.bias, DT_F16, co) : 0.f;
+        const float sc = p.scale ? ld(p.scale, DT_F16, co) : 1.f;
+        const size_t obase = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo;
+        for (uint32_t wo = lane; wo < p.wo; wo += 64) {
+            float v = red[(size_t)col * rw + wo] + red[((size_t)CO_TILE + col) * rw + wo] +
+                      red[((size_t)2 * CO_TILE + col) * rw + wo] + red[((size_t)3 * CO_TILE + col) * rw + wo];
+            v = p.scale ? fmaf(v, sc, bias) : v + bias;
+            const size_t o = obase + wo;
+            const float rr = p.residual ? ld(p.residual, p.residual_dtype, o) : 0.f;
+            if (p.residual && p.residual_order == 1) v += rr;
+            v = epilogue(v, p.epilogue);
+            if (p.residual && p.residual_order == 0) v += rr;
+            st(p.out, p.o_dtype, o, v);
+        }
+    }
+}
+
+size_t conv_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks)
+{
+    const size_t WiP = wi + 2 * (ks / 2), CIP = cv::cip(ci);
+    const size_t stage = (size_t)ks * WiP * CIP * 2;
+    const size_t red = 4ull * cv::CO_TILE * 16 * cv::MAX_WO_FRAGS * 4;
+    return stage > red ? stage : red;
+}
+
+bool conv_nhwc_ok(uint32_t ci, uint32_t wi, uint32_t wo, uint32_t ks)
+{
+    return (ks == 1 || ks == 3) && wo <= 16u * cv::MAX_WO_FRAGS &&
+           conv_lds_bytes(ci, wi, ks) <= 160u * 1024u && (size_t)ci * ks * ks * 2 <= 64u * 1024u;
+}
+
+size_t conv_packed_weight_bytes(uint32_t ci, uint32_t co, uint32_t ks)
+{
+    return (size_t)ks * ks * co * cv::ci32(ci) * 2;
+}
+
+hipError_t conv_pack_weight(half_t* dst, const half_t* w, uint32_t ci, uint32_t co, uint32_t ks, hipStream_t s)
+{
+    hipLaunchKernelGGL(pack_weight_kernel, dim3(co), dim3(256), (size_t)ci * ks * ks * 2, s, dst, w, co, ci,
+                       cv::ci32(ci), ks * ks);
+    return hipGetLastError();
+}
+
+template <int KS, int NF>
+static hipError_t launch_nf(const ConvParams& p, int x_dt, size_t lds, hipStream_t s)
+{
+    auto kern = x_dt == DT_F16 ? conv_kernel<KS, NF, half_t> : conv_kernel<KS, NF, float>;
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((p.co + cv::CO_TILE - 1) / cv::CO_TILE, p.ho, p.batch), dim3(512), lds, s, p);
+    return hipGetLastError();
+}
+
+template <int KS>
+static hipError_t launch_ks(const ConvParams& p, int x_dt, size_t lds, hipStream_t s)
+{
+    switch ((p.wo + 15) / 16) {
+    case 1: return launch_nf<KS, 1>(p, x_dt, lds, s);
+    case 2: return launch_nf<KS, 2>(p, x_dt, lds, s);
+    case 3: return launch_nf<KS, 3>(p, x_dt, lds, s);
+    case 4: return launch_nf<KS, 4>(p, x_dt, lds, s);
+    case 5: return launch_nf<KS, 5>(p, x_dt, lds, s);
+    case 6: return launch_nf<KS, 6>(p, x_dt, lds, s);
+    case 7: return launch_nf<KS, 7>(p, x_dt, lds, s);
+    default: return launch_nf<KS, 8>(p, x_dt, lds, s);
+    }
+}
+
+hipError_t conv_launch(const ConvParams& p, int x_dt, hipStream_t s)
+{
+    const size_t lds = conv_lds_bytes(p.ci, p.wi, p.ks);
+    return p.ks == 1 ? launch_ks<1>(p, x_dt, lds, s) : launch_ks<3>(p, x_dt, lds, s);
+}
+
+}   // namespace vai_dev

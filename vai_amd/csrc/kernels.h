@@ -7,6 +7,8 @@
 
 namespace vai_dev {
 
+typedef _Float16 half_t_storage;
+
 struct SlabParams {
     void* out;
     const void* in;
@@ -75,6 +77,24 @@ hipError_t gemm_launch(const GemmParams& p, BKind bk, EpiKind ek, GemmTile tile,
 // The 256x256x64 fp16 MFMA GEMM for large, K%64 == 0 shapes (Linear / gated).
 bool gemm_big_ok(const GemmParams& p, bool gated);
 hipError_t gemm_big_launch(const GemmParams& p, bool gated, hipStream_t s);
+
+// Implicit-GEMM convolution, fp16 weights packed [tap][Co][C32].
+struct ConvParams {
+    void* out;
+    const void* x;                // input [B][Ci][Hi][Wi], fp16 or fp32
+    const half_t_storage* wp;     // packed weight [k*k][Co][C32]
+    const void* bias;             // fp16 [Co] or null
+    const void* scale;            // fp16 [Co] or null
+    const void* residual;         // [B][Co][Ho][Wo] (residual_dtype) or null
+    int o_dtype, residual_dtype;
+    uint32_t batch, ci, hi, wi, co, ho, wo, ks, stride;
+    uint32_t epilogue, residual_order;
+};
+bool conv_nhwc_ok(uint32_t ci, uint32_t wi, uint32_t wo, uint32_t ks);
+size_t conv_packed_weight_bytes(uint32_t ci, uint32_t co, uint32_t ks);
+hipError_t conv_pack_weight(half_t_storage* dst, const half_t_storage* w, uint32_t ci, uint32_t co, uint32_t ks,
+                            hipStream_t s);
+hipError_t conv_launch(const ConvParams& p, int x_dt, hipStream_t s);
 
 // Split-K fold for Linear: O = s*epi(sum_z P[z] + B) (+R).
 hipError_t linear_reduce_launch(void* out, int o_dtype, const float* partials, uint32_t splits, size_t MN,

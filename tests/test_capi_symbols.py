@@ -66,7 +66,8 @@ def test_plans():
             setattr(a, key, v)
         return _capi.linear_plan(a)
     assert plan(1, 8192, 2048) == ("slab", 1)
-    assert plan(8, 8192, 2048)[0] == "slab"
+    assert plan(8, 8192, 2048)[0] == "slab_mfma"
+    assert plan(8, 8192, 2048, np.float32, np.float16)[0] == "slab"
     assert plan(8, 8192, 2047)[0] == "slab_scalar"
     assert plan(9, 8192, 2048)[0].startswith("tile_f16")
     assert plan(128, 3072, 768, np.float32, np.float32)[0].startswith("tile_f32")

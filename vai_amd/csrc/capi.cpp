@@ -146,7 +146,8 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
     if (p.kind == LinearPlan::Slab || p.kind == LinearPlan::SlabThenGate) {
         SlabParams sp{};
         sp.K = a->K; sp.w_dtype = a->w_dtype; sp.i_dtype = a->i_dtype; sp.weight = a->weight; sp.in = a->in;
-        snprintf(buf, sizeof buf, "%s%s", slab_vec_ok(sp) ? "slab" : "slab_scalar",
+        sp.M = a->M;
+        snprintf(buf, sizeof buf, "%s%s", (sp.M >= 2 && gemv_mfma_ok(sp)) ? "slab_mfma" : slab_vec_ok(sp) ? "slab" : "slab_scalar",
                  p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
     } else if (p.kind == LinearPlan::BigTile) {
         snprintf(buf, sizeof buf, "tile_f16_256x256%s", a->gated ? "_gated" : "");

@@ -21,6 +21,7 @@ struct SlabParams {
     float scalar_scale;
 };
 bool slab_vec_ok(const SlabParams& a);
+bool gemv_mfma_ok(const SlabParams& a);
 hipError_t slab_launch(const SlabParams& a, hipStream_t s);
 
 // The operand a GEMM's "B" side reads: C[M,N] = A[M,K] . B[N,K]^T.

@@ -21,27 +21,49 @@ template <typename T> struct Vec16;
 template <> struct Vec16<half_t> { typedef half8 type; static constexpr int n = 8; };
 template <> struct Vec16<float> { typedef float4v type; static constexpr int n = 4; };
 
+// x + (x of the lane the DPP control names); all 64 lanes take part.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x)
+{
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true);
+    return x + __builtin_bit_cast(float, moved);
+}
+
+// Sum over the lane bits below LIMIT, lowest first: bits 0-3 stay inside a
+// row of 16 lanes and go through DPP (quad_perm 1032, quad_perm 2301,
+// row_half_mirror, row_mirror: after the lower bits are summed, each of
+// these pairs lanes that differ in the next bit); bits 4 and 5 use shuffles.
+template <int LIMIT>
+__device__ __forceinline__ float lane_sum_low(float x)
+{
+    if constexpr (LIMIT > 1) x = dpp_add<0xB1>(x);
+    if constexpr (LIMIT > 2) x = dpp_add<0x4E>(x);
+    if constexpr (LIMIT > 4) x = dpp_add<0x141>(x);
+    if constexpr (LIMIT > 8) x = dpp_add<0x140>(x);
+    if constexpr (LIMIT > 16) x += __shfl_xor(x, 16, 64);
+    if constexpr (LIMIT > 32) x += __shfl_xor(x, 32, 64);
+    return x;
+}
+
 // Butterfly over a wave of CNT values per lane: at offset O a lane keeps the
 // half selected by (lane & O) and adds its partner's copy of that half, so
-// each exchange halves the values per lane; once one is left, plain xor-adds.
+// each exchange halves the values per lane; once one is left, the lane bits
+// below O are summed by lane_sum_low.
 template <int CNT, int O>
 __device__ __forceinline__ void butterfly(float* acc, int lane)
 {
-    if constexpr (O >= 1) {
-        if constexpr (CNT > 1) {
-            constexpr int H = CNT / 2;
-            const bool upper = (lane & O) != 0;
+    if constexpr (CNT > 1) {
+        constexpr int H = CNT / 2;
+        const bool upper = (lane & O) != 0;
 #pragma unroll
-            for (int i = 0; i < H; ++i) {
-                const float send = upper ? acc[i] : acc[i + H];
-                const float keep = upper ? acc[i + H] : acc[i];
-                acc[i] = keep + __shfl_xor(send, O, 64);
-            }
-            butterfly<H, O / 2>(acc, lane);
-        } else {
-            acc[0] += __shfl_xor(acc[0], O, 64);
-            butterfly<1, O / 2>(acc, lane);
+        for (int i = 0; i < H; ++i) {
+            const float send = upper ? acc[i] : acc[i + H];
+            const float keep = upper ? acc[i + H] : acc[i];
+            acc[i] = keep + __shfl_xor(send, O, 64);
         }
+        butterfly<H, O / 2>(acc, lane);
+    } else {
+        acc[0] = lane_sum_low<O * 2>(acc[0]);
     }
 }
 
@@ -78,7 +100,7 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
     constexpr int KB = 64 * KCH * EPC;     // K elements per block iteration
     constexpr int V = MP * R;              // dot products per lane
     static_assert(V <= 64 && (V & (V - 1)) == 0, "butterfly needs a power of two <= 64");
-    __shared__ TI xs[MP * KB];
+    __shared__ TI xs[MP <= 2 ? 1 : MP * KB];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -104,31 +126,52 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
                 else
                     wv[r][c] = (wvec)0;
             }
-        // 2. The M input rows of this block into LDS (zero past K and past M).
-        __syncthreads();
-        for (uint32_t i = threadIdx.x * EPC; i < (uint32_t)(MP * KB); i += 256 * EPC) {
-            const uint32_t m = i / KB, kk = kb + (i % KB);
-            // EPC elements of X per thread: K % EPC == 0 keeps them in one row.
-            typedef TI xvec __attribute__((ext_vector_type(EPC)));
-            xvec v = (m < M && kk < K) ? *(const xvec*)(X + (size_t)m * K + kk) : (xvec)0;
-            *(xvec*)(xs + i) = v;
-        }
-        __syncthreads();
-        // 3. Dot products.
+        if constexpr (MP <= 2) {
+            // 2'. Few input rows: each lane loads its own X chunks (L2-resident)
+            //     straight into registers; no LDS, no barrier.
 #pragma unroll
-        for (int c = 0; c < KCH; ++c) {
+            for (int c = 0; c < KCH; ++c) {
+                const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
 #pragma unroll
-            for (int m = 0; m < MP; ++m) {
-                float xf[EPC];
-                const TI* xp = xs + m * KB + (c * 64 + lane) * EPC;
+                for (int m = 0; m < MP; ++m) {
+                    typedef TI xvec __attribute__((ext_vector_type(EPC)));
+                    const xvec xv = ((uint32_t)m < M && k < K) ? *(const xvec*)(X + (size_t)m * K + k) : (xvec)0;
 #pragma unroll
-                for (int e = 0; e < EPC; ++e) xf[e] = (float)xp[e];
+                    for (int r = 0; r < R; ++r) {
+                        float s = acc[m * R + r];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float s = acc[m * R + r];
+                        for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], (float)xv[e], s);
+                        acc[m * R + r] = s;
+                    }
+                }
+            }
+        } else {
+            // 2. The M input rows of this block into LDS (zero past K and past M).
+            __syncthreads();
+            for (uint32_t i = threadIdx.x * EPC; i < (uint32_t)(MP * KB); i += 256 * EPC) {
+                const uint32_t m = i / KB, kk = kb + (i % KB);
+                // EPC elements of X per thread: K % EPC == 0 keeps them in one row.
+                typedef TI xvec __attribute__((ext_vector_type(EPC)));
+                xvec v = (m < M && kk < K) ? *(const xvec*)(X + (size_t)m * K + kk) : (xvec)0;
+                *(xvec*)(xs + i) = v;
+            }
+            __syncthreads();
+            // 3. Dot products.
 #pragma unroll
-                    for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], xf[e], s);
-                    acc[m * R + r] = s;
+            for (int c = 0; c < KCH; ++c) {
+#pragma unroll
+                for (int m = 0; m < MP; ++m) {
+                    float xf[EPC];
+                    const TI* xp = xs + m * KB + (c * 64 + lane) * EPC;
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) xf[e] = (float)xp[e];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float s = acc[m * R + r];
+#pragma unroll
+                        for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], xf[e], s);
+                        acc[m * R + r] = s;
+                    }
                 }
             }
         }
@@ -174,11 +217,66 @@ __global__ __launch_bounds__(256) void slab_scalar_kernel(SlabParams a)
     }
 }
 
+// fp16 I and W, M <= 16: the GEMV on v_mfma_f32_16x16x32_f16. A = I padded
+// to 16 rows (rows >= M read as zero), B = 16 rows of W. fp16 products are
+// exact in fp32 and accumulate in fp32, the slab contract, while the matrix
+// core keeps the arithmetic off the VALU: at M = 8 the FMA path costs more
+// than the 32 MB HBM stream it overlaps. A workgroup owns 16 W rows; its 4
+// waves take a quarter of K each, issue all their 16-byte non-temporal W
+// loads up front, and sum their 16x16 partials through LDS.
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(SlabParams a)
+{
+    constexpr int BATCH = 16;                     // 16-byte W loads per lane in flight
+    __shared__ float part[4][16][17];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t n0 = blockIdx.x * 16, K = a.K, N = a.N, M = a.M;
+    const int fr = lane & 15, fg = lane >> 4;
+    const uint32_t kq = K / 4, kbeg = wave * kq;
+    const half_t* __restrict__ W = (const half_t*)a.weight;
+    const half_t* __restrict__ X = (const half_t*)a.in;
+    const uint32_t wrow = min(n0 + fr, N - 1);
+    const half_t* wp = W + (size_t)wrow * K + kbeg + fg * 8;
+    const bool xrow_ok = (uint32_t)fr < M;
+    const half_t* xp = X + (size_t)(xrow_ok ? fr : 0) * K + kbeg + fg * 8;
+    float4v acc = (float4v)0.f;
+    for (uint32_t k = 0; k < kq; k += 32 * BATCH) {
+        half8 wv[BATCH], xv[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i)
+            wv[i] = (k + i * 32 < kq) ? __builtin_nontemporal_load((const half8*)(wp + k + i * 32)) : (half8)0;
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i)
+            xv[i] = (xrow_ok && k + i * 32 < kq) ? *(const half8*)(xp + k + i * 32) : (half8)0;
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[i], wv[i], acc, 0, 0, 0);
+    }
+    // D[i][j] (i = input row m, j = W row) sits in lane j + 16*(i/4), register i%4.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[wave][fg * 4 + r][fr] = acc[r];
+    __syncthreads();
+    const int m = threadIdx.x / 16, j = threadIdx.x % 16;
+    if ((uint32_t)m < M && n0 + j < N) {
+        const float v = part[0][m][j] + part[1][m][j] + part[2][m][j] + part[3][m][j];
+        const size_t o = (size_t)m * N + n0 + j;
+        const float b = a.bias ? ld(a.bias, a.b_dtype, a.bias_repeat ? o % a.bias_repeat : o) : 0.f;
+        const float rr = a.residual ? ld(a.residual, a.o_dtype, a.residual_repeat ? o % a.residual_repeat : o) : 0.f;
+        st(a.out, a.o_dtype, o, finish(v + b, rr, a.epilogue, a.residual_order, a.scalar_scale));
+    }
+}
+
+bool gemv_mfma_ok(const SlabParams& a)
+{
+    return a.i_dtype == DT_F16 && a.w_dtype == DT_F16 && a.M <= 16 && a.K % 128 == 0 &&
+           ((uintptr_t)a.weight % 16) == 0 && ((uintptr_t)a.in % 16) == 0;
+}
+
 template <int MP, typename TI, typename TW>
 static hipError_t launch_vec(const SlabParams& a, hipStream_t s)
 {
-    // R rows per wave: 4 keeps 16 loads of 16 B in flight per lane at KCH 4.
-    constexpr int R = 4, KCH = 4;
+    // R rows per wave x KCH chunks per lane: 2 x 4 (8 loads of 16 B in flight
+    // per lane, 4096 waves at the config-2 shape) measured fastest on MI355X
+    // among 1..8 x 2..8.
+    constexpr int R = 2, KCH = 4;
     const uint32_t blocks = (a.N + 4 * R - 1) / (4 * R);
     hipLaunchKernelGGL((slab_vec_kernel<MP, R, KCH, TI, TW>), dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();
@@ -202,6 +300,10 @@ bool slab_vec_ok(const SlabParams& a)
 
 hipError_t slab_launch(const SlabParams& a, hipStream_t s)
 {
+    if (a.M >= 2 && gemv_mfma_ok(a)) {
+        hipLaunchKernelGGL(gemv_mfma_kernel, dim3((a.N + 15) / 16), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     if (slab_vec_ok(a)) {
         switch (a.M) {
         case 1: return launch_m<1>(a, s);

@@ -324,6 +324,7 @@ vai_status vai_attn_scores_launch(const vai_attn_scores_args* a, vai_stream_t st
     g.split_size = g.K; g.splits = 1;
     g.scalar_scale = a->scale; g.causal = a->causal; g.span = a->span;
     g.causal_offset = (int32_t)a->tkv - (int32_t)a->tq;
+    if (scores_fast_ok(g)) return hip_status(scores_launch(g, (hipStream_t)stream));
     const GemmTile t = tiles_of(g.M, g.N, 128, 128) * g.batch >= kCUs ? GemmTile::T128x128 : GemmTile::T64x64;
     return hip_status(gemm_launch(g, BKind::Dense, EpiKind::Scores, t, (hipStream_t)stream));
 }

@@ -79,6 +79,10 @@ hipError_t gemm_launch(const GemmParams& p, BKind bk, EpiKind ek, GemmTile tile,
 bool gemm_big_ok(const GemmParams& p, bool gated);
 hipError_t gemm_big_launch(const GemmParams& p, bool gated, hipStream_t s);
 
+// Attention scores for fp16 Q/K with head_dim % 64 == 0.
+bool scores_fast_ok(const GemmParams& p);
+hipError_t scores_launch(const GemmParams& p, hipStream_t s);
+
 // Implicit-GEMM convolution, fp16 weights packed [tap][Co][C32].
 struct ConvParams {
     void* out;

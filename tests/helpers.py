@@ -52,3 +52,23 @@ def assert_close(got, want, tol, what=""):
     assert np.array_equal(np.isinf(got), same_inf), f"{what}: -inf pattern differs"
     assert (got[same_inf] == want[same_inf]).all(), f"{what}: inf sign differs"
     np.testing.assert_allclose(got[~same_inf], want[~same_inf], rtol=tol[0], atol=tol[1], err_msg=what)
+
+
+def np_epilogue(name, y):
+    """float64 closed forms of the reference's epilogues (activation.h:19-58)."""
+    import math
+    y = np.asarray(y, np.float64)
+    if name == "NONE":
+        return y
+    if name == "RELU":
+        return np.maximum(y, 0)
+    if name == "GELU":
+        erf = np.vectorize(math.erf)
+        return 0.5 * y * (1 + erf(y / math.sqrt(2)))
+    if name == "GELU_TANH":
+        return 0.5 * y * (1 + np.tanh(math.sqrt(2 / math.pi) * (y + 0.044715 * y ** 3)))
+    if name == "SILU":
+        return y / (1 + np.exp(-y))
+    if name == "SIGMOID":
+        return 1 / (1 + np.exp(-y))
+    raise ValueError(name)

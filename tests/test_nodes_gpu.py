@@ -1,0 +1,172 @@
+"""Nodes through the engine on the MI355X, as the reference tests them
+(/root/reference/python/tests/nodes/test_linear.py:11-84,
+test_convolution.py:12-87, test_gated_mul.py): one-node nets built with the
+`-` wiring DSL, float64 expectations, a bit-identical replayed second forward,
+and a rerun on other shapes. Plus what is new here: the record-once/replay
+graph, the Linear -> GatedMul fusion, the attention-scores node.
+"""
+import numpy as np
+import pytest
+
+from helpers import FP16, FP32, TRANS, assert_close, draw, normal, np_epilogue, uniform
+from node_check import build_net, check_node, forward, pyvai
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize(
+    "m, k, n, has_bias, epilogue, split_size, tol, alt_m",
+    [
+        (1, 64, 32, True, "NONE", 0, FP32, 33),   # rerun: slab -> tile
+        (8, 96, 40, False, "NONE", 0, FP32, None),
+        (33, 96, 48, True, "RELU", 0, FP32, None),
+        (64, 128, 100, False, "GELU_TANH", 0, TRANS, None),
+        (16, 256, 64, True, "NONE", 64, FP32, None),
+        (33, 1000, 100, True, "NONE", 0, FP32, None),
+        (33, 100, 48, False, "NONE", 0, FP32, None),
+        (33, 102, 48, False, "NONE", 0, FP32, None),
+        (33, 101, 48, False, "NONE", 0, FP32, None),
+        (16, 2050, 64, True, "NONE", 0, FP32, None),
+        (33, 1000, 48, False, "NONE", 100, FP32, None),
+    ],
+)
+def test_linear_node(gpu, m, k, n, has_bias, epilogue, split_size, tol, alt_m):
+    pv = pyvai()
+    params = {"weight": normal((n, k), 1.0 / np.sqrt(k))}
+    if has_bias:
+        params["bias"] = (n,)
+
+    def ref(in0, weight, bias=None):
+        y = in0.astype(np.float64) @ weight.astype(np.float64).T
+        if bias is not None:
+            y = y + bias
+        return np_epilogue(epilogue, y)
+
+    check_node(lambda: pv.nodes.LinearNode(in_dim=k, out_dim=n, epilogue=getattr(pv.Epilogue, epilogue),
+                                           split_size=split_size),
+               {"in0": (m, k)}, ref, params=params, tol=tol,
+               alt_inputs={"in0": (alt_m, k)} if alt_m else None)
+
+
+@pytest.mark.parametrize("m, order", [(4, "AFTER_EPILOGUE"), (4, "BEFORE_EPILOGUE"),
+                                      (33, "AFTER_EPILOGUE"), (33, "BEFORE_EPILOGUE")])
+def test_linear_node_residual(gpu, m, order):
+    pv = pyvai()
+    k, n = 64, 48
+
+    def ref(in0, residual, weight, bias):
+        y = in0.astype(np.float64) @ weight.astype(np.float64).T + bias
+        if order == "BEFORE_EPILOGUE":
+            return np.maximum(y + residual, 0)
+        return np.maximum(y, 0) + residual
+
+    check_node(lambda: pv.nodes.LinearNode(in_dim=k, out_dim=n, accept_residual=True,
+                                           residual_order=getattr(pv.ResidualOrder, order), epilogue=pv.Epilogue.RELU),
+               {"in0": (m, k), "residual": (m, n)}, ref,
+               params={"weight": normal((n, k), 1.0 / np.sqrt(k)), "bias": (n,)}, tol=FP32)
+
+
+@pytest.mark.parametrize("ci, co, ks, stride, hw, epi, w16", [
+    (16, 32, 1, 1, 12, "NONE", False), (8, 16, 3, 1, 12, "RELU", False), (8, 16, 3, 1, 28, "SILU", False),
+    (8, 16, 3, 2, 13, "NONE", False), (4, 8, 5, 1, 11, "GELU", False), (32, 48, 3, 1, 20, "SILU", True),
+    (24, 40, 1, 1, 17, "SIGMOID", True)])
+def test_convolution_node(gpu, ci, co, ks, stride, hw, epi, w16):
+    pv = pyvai()
+    dts = {"weight": np.float16, "bias": np.float16, "in0": np.float16} if w16 else {}
+
+    def ref(in0, weight, bias):
+        return np.asarray(oracle.conv2d(in0, weight, bias, stride=stride, epi=epi), np.float64)
+
+    check_node(lambda: pv.nodes.ConvolutionNode(in_channels=ci, out_channels=co, kernel_size=ks, stride=stride,
+                                                epilogue=getattr(pv.Epilogue, epi)),
+               {"in0": (2, ci, hw, hw)}, ref,
+               params={"weight": normal((co, ci, ks, ks), 1.0 / np.sqrt(ci * ks * ks)), "bias": normal((co,), 0.1)},
+               tol=FP16 if w16 else TRANS, input_dtypes=dts,
+               alt_inputs={"in0": (1, ci, hw + 2, hw + 1)},
+               net_kw={"w_dtype": "F16" if w16 else "F32"})
+
+
+def test_gated_mul_node(gpu):
+    pv = pyvai()
+    check_node(lambda: pv.nodes.GatedMulNode(activation=pv.Epilogue.GELU), {"in0": (5, 2 * 24)},
+               lambda in0: np_epilogue("GELU", in0[:, :24]) * in0[:, 24:], tol=TRANS)
+
+
+def _ffn_net(pv, k, h, fuse):
+    class Net(pv.NeuralNet):
+        def __init__(self):
+            super().__init__(w_default_dtype=pv.Dtype.F16, fuse_gated_linear=fuse)
+            self.gate_up = pv.nodes.LinearNode(in_dim=k, out_dim=2 * h)
+            self.glu = pv.nodes.GatedMulNode(activation=pv.Epilogue.SILU)
+            self.input("in0") - self.gate_up - self.glu - self.output("out0")
+    return Net()
+
+
+@pytest.mark.parametrize("m, k, h", [(6, 256, 96), (300, 512, 160), (1024, 512, 512)])
+def test_gated_ffn_fusion(gpu, m, k, h):
+    """gate/up Linear -> GatedMul (gated-feed-forward.h:37-46): fused at record
+    time into one gated GEMM; same result as the two-kernel path."""
+    pv = pyvai()
+    rng = np.random.default_rng(0)
+    w = draw(normal((2 * h, k), 0.05), rng, np.float16)
+    b = draw(normal((2 * h,), 0.05), rng, np.float16)
+    x = draw((m, k), rng, np.float16)
+    outs = {}
+    for fuse in (True, False):
+        net = _ffn_net(pv, k, h, fuse)
+        net.gate_up["weight"] = pv.Tensor.from_numpy(w)
+        net.gate_up["bias"] = pv.Tensor.from_numpy(b)
+        outs[fuse] = forward(net, {"in0": x})
+        assert net.gate_up.fused == fuse
+    want = oracle.gated_mul(oracle.linear(x, w, b), epi="SILU")
+    assert_close(outs[True], want, TRANS)
+    assert_close(outs[False], want, TRANS)
+
+
+def test_replay_and_rerecord(gpu):
+    """Same shapes replay the recorded HIP graph; a new shape records again."""
+    pv = pyvai()
+    rng = np.random.default_rng(0)
+    w = draw(normal((64, 128), 0.1), rng)
+    net = build_net(lambda: pv.nodes.LinearNode(in_dim=128, out_dim=64, epilogue=pv.Epilogue.SILU), ["in0"],
+                    {"weight": w})
+    x1, x2, x3 = (draw((40, 128), rng) for _ in range(3))
+    y1 = forward(net, {"in0": x1})
+    assert net.record_count == 1
+    y2 = forward(net, {"in0": x2})                   # new data, same shape: replay
+    assert net.record_count == 1
+    assert_close(y2, oracle.linear(x2, w, epi="SILU"), TRANS)
+    y3 = forward(net, {"in0": x3[:7]})               # new shape: record again (and the slab path)
+    assert net.record_count == 2
+    assert_close(y3, oracle.linear(x3[:7], w, epi="SILU"), TRANS)
+    assert_close(y1, oracle.linear(x1, w, epi="SILU"), TRANS)
+    assert net.submit_count == 3
+
+
+@pytest.mark.parametrize("hq, hkv, tq, tkv, d, causal", [(4, 4, 64, 64, 64, True), (4, 2, 50, 80, 128, True),
+                                                         (2, 1, 33, 33, 32, False)])
+def test_attention_scores_node(gpu, hq, hkv, tq, tkv, d, causal):
+    pv = pyvai()
+    rng = np.random.default_rng(0)
+    q = draw((2, hq, tq, d), rng, np.float16)
+    k = draw((2, hkv, tkv, d), rng, np.float16)
+    net = build_net(lambda: pv.nodes.AttentionScoresNode(num_q_heads=hq, head_dim=d, num_kv_heads=hkv, causal=causal),
+                    ["in0", "K"], {})
+    got = forward(net, {"in0": q, "K": k})
+    assert_close(got, oracle.attn_scores(q, k, causal=causal), FP32)
+
+
+def test_gpt2_cfc_through_the_engine(gpu):
+    """BASELINE config 1 via input - linear - output."""
+    import os, sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import configs as C
+    G = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "baseline_configs.npz"))
+    pv = pyvai()
+    x, w, b = C.cfg1()
+    net = build_net(lambda: pv.nodes.LinearNode(in_dim=768, out_dim=3072, epilogue=pv.Epilogue.GELU_TANH), ["in0"],
+                    {"weight": w, "bias": b})
+    got = forward(net, {"in0": x})
+    assert net.node.plan.startswith("tile_f32")
+    assert_close(got[C.CFG1_ROWS], G["cfg1_rows"], FP32)

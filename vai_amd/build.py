@@ -22,14 +22,39 @@ COMMON = ["-O3", "-fPIC", "-std=c++20", f"--offload-arch={ARCH}", "-I", os.path.
           "-I", HERE, "-Wno-pass-failed"]
 
 
+PYMOD_SRC = os.path.join(ENGINE, "pyvai.cpp")
+
+
 def _sources():
     srcs = []
     for d in (CSRC, ENGINE):
         if os.path.isdir(d):
             for f in sorted(os.listdir(d)):
-                if f.endswith((".hip", ".cpp")):
+                if f.endswith((".hip", ".cpp")) and os.path.join(d, f) != PYMOD_SRC:
                     srcs.append(os.path.join(d, f))
     return srcs
+
+
+def _build_pymodule():
+    """pybind11 module _pyvai (the engine's Python surface), linked to libvai_amd.so."""
+    import sysconfig
+    import pybind11
+    ext = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(HERE, "_pyvai" + ext)
+    obj = os.path.join(BUILD, "pyvai.o")
+    inc = ["-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"]]
+    cmd = [HIPCC, "-x", "hip", "-O2", "-fPIC", "-std=c++20", f"--offload-arch={ARCH}", "-I",
+           os.path.join(ROOT, "include"), "-I", HERE] + inc + ["-c", PYMOD_SRC, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("pyvai compile failed:\n" + r.stderr)
+    tmp = out + ".tmp"
+    cmd = [HIPCC, "-shared", "-o", tmp, obj, "-L", HERE, "-lvai_amd", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("pyvai link failed:\n" + r.stderr)
+    os.replace(tmp, out)
+    return out
 
 
 def _compile(src):
@@ -56,6 +81,7 @@ def build(jobs=None):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
     os.replace(tmp, LIB)
+    _build_pymodule()
     return LIB
 
 

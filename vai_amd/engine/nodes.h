@@ -1,0 +1,146 @@
+// nodes.h -- the matmul-path nodes of the reference, on the MI355X kernels.
+//   Linear        /root/reference/vai/nodes/linear.h:59-348
+//   GatedMul      /root/reference/vai/nodes/gated-mul.h:21-44
+//   Convolution   /root/reference/vai/nodes/convolution.h:2453-2609
+//   AttentionScores  the S = scale * Q.K^T (+ causal mask) stage of
+//                 /root/reference/vai/nodes/attention.h:144-280, as a node of
+//                 its own (the reference fuses it into flash attention).
+// Configs keep the reference's field names and defaults; prepare() validates
+// and picks the kernel through the C ABI, run() launches on the net's stream.
+#pragma once
+#include <cstdint>
+
+#include "../../include/vai_amd.h"
+#include "graph-flow.h"
+#include "neural-net.h"
+
+namespace vai {
+
+// /root/reference/vai/nodes/common.h:31-45.
+enum class Epilogue : uint32_t { None, Relu, Gelu, GeluTanh, Silu, Sigmoid, Max };
+enum class ResidualOrder : uint32_t { AfterEpilogue = 0, BeforeEpilogue = 1 };
+
+// The product of the axes ahead of the last innerAxes (common.h:67-73).
+inline uint32_t outerSize(const std::vector<uint32_t>& shape, size_t innerAxes = 1)
+{
+    uint32_t n = 1;
+    for (size_t i = 0; i + innerAxes < shape.size(); ++i) n *= shape[i];
+    return n;
+}
+
+namespace node {
+
+class GatedMul;
+
+class Linear : public Node
+{
+public:
+    struct Config {
+        uint32_t inDim;
+        uint32_t outDim;
+        bool acceptResidual = false;
+        ResidualOrder residualOrder = ResidualOrder::AfterEpilogue;
+        Epilogue epilogue = Epilogue::None;
+        float scalarScale = 1.0f;
+        uint32_t splitSize = 0;   // split-K span; 0 lets the library choose per shape
+    } config_;
+
+    explicit Linear(Config config);
+    void prepare() override;
+    void run(CommandStream& cmd) override;
+    const char* kind() const override { return "Linear"; }
+
+    bool hasBias() const { return (*this)["bias"].validShape(); }
+    // The kernels accumulate in fp32 whatever is asked: fp32 is the reference's
+    // AMD default (linear.h:2320) and an fp16 request only narrows precision.
+    void setAccDtype(Dtype dtype, DtypeKey) { accDtype_ = dtype; }
+    Dtype accDtype() const { return accDtype_; }
+
+    // The kernel prepare() chose ("slab", "tile_f16_256x256_gated", ...) and its split count.
+    const std::string& plan() const { return plan_; }
+    uint32_t splitCount() const { return splitCount_; }
+
+    // Record-time fusion with a following GatedMul (see NeuralNet::bindFusion).
+    bool canFuseGate(const GatedMul& gm) const;
+    void setFusedGate(GatedMul* gm) { fused_ = gm; }
+    GatedMul* fusedGate() const { return fused_; }
+
+private:
+    Dtype accDtype_ = Dtype::None;
+    GatedMul* fused_ = nullptr;
+    uint32_t M_ = 0, biasRepeat_ = 0, residualRepeat_ = 0;
+    std::string plan_;
+    uint32_t splitCount_ = 1;
+    vai_linear_args args(bool withPointers) const;
+};
+
+class GatedMul : public Node
+{
+    friend class Linear;
+
+public:
+    struct Config {
+        Epilogue activation = Epilogue::Silu;
+    } config_;
+
+    GatedMul();
+    explicit GatedMul(Config config);
+    void prepare() override;
+    void run(CommandStream& cmd) override;
+    const char* kind() const override { return "GatedMul"; }
+
+private:
+    bool fusedInto() const;
+};
+
+class Convolution : public Node
+{
+public:
+    struct Config {
+        uint32_t inChannels;
+        uint32_t outChannels;
+        uint32_t kernelSize;
+        uint32_t stride;
+        bool acceptResidual = false;
+        ResidualOrder residualOrder = ResidualOrder::AfterEpilogue;
+        Epilogue epilogue = Epilogue::None;
+    } config_;
+
+    explicit Convolution(Config config);
+    void prepare() override;
+    void run(CommandStream& cmd) override;
+    const char* kind() const override { return "Convolution"; }
+
+    bool hasBias() const { return (*this)["bias"].validShape(); }
+    bool hasScale() const { return (*this)["scale"].validShape(); }
+
+private:
+    vai_conv2d_args args(bool withPointers) const;
+    PooledBuffer packed_;          // weight packed once for the fp16 kernel
+    const void* packedFrom_ = nullptr;
+    uint32_t batch_ = 1, hi_ = 0, wi_ = 0;
+};
+
+class AttentionScores : public Node
+{
+public:
+    struct Config {
+        uint32_t numQHeads;
+        uint32_t numKVHeads = 0;   // 0: numQHeads (no GQA)
+        uint32_t headDim;
+        bool causal = true;
+        uint32_t span = 0;         // sliding window; 0: none
+        float scale = 0.0f;        // 0: 1/sqrt(headDim), as attention.h:1254
+    } config_;
+
+    explicit AttentionScores(Config config);
+    void prepare() override;
+    void run(CommandStream& cmd) override;
+    const char* kind() const override { return "AttentionScores"; }
+
+private:
+    uint32_t batch_ = 1, tq_ = 0, tkv_ = 0;
+};
+
+}   // namespace node
+}   // namespace vai

@@ -29,6 +29,12 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 ROTATE_BYTES = 384 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.tsv")
+# rocprofv3 counter scale factors on gfx950, measured with GatedMul over a
+# [4096, 4096] fp32 input (reads exactly 64 MiB, writes 32 MiB): FETCH_SIZE
+# reports half the bytes read, WRITE_SIZE reports the bytes written.
+FETCH_FACTOR = 2.0
+WRITE_FACTOR = 1.0
 
 
 def parse():
@@ -40,6 +46,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--repeats", type=int, default=3)
+    ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
+                    help="counter-collection mode: a calibration kernel of known traffic, then REPS "
+                         "untimed launches of each workload; prints nothing else")
     return ap.parse_args()
 
 
@@ -50,10 +59,25 @@ def f16(a):
 class Case:
     """One configuration: device buffers, one step's launches, its work."""
 
-    def __init__(self, name, unit, work, bound, peak, launch_fn, kernel, flops, bytes_, dtype):
+    def __init__(self, name, unit, work, bound, peak, launch_fn, kernel, flops, bytes_, dtype, tkey):
         self.name, self.unit, self.work, self.bound, self.peak = name, unit, work, bound, peak
         self.launch = launch_fn      # launch(step_index) -> None, on the bench stream
         self.kernel, self.flops, self.bytes, self.dtype = kernel, flops, bytes_, dtype
+        self.tkey = tkey             # row of the traffic table for this workload
+
+
+def load_traffic():
+    """HBM bytes per launch from the committed rocprofv3 counter table:
+    workload key -> FETCH_FACTOR * FETCH_SIZE + WRITE_FACTOR * WRITE_SIZE."""
+    out = {}
+    if not os.path.exists(TRAFFIC_FILE):
+        return out
+    for ln in open(TRAFFIC_FILE):
+        if ln.startswith("#") or not ln.strip():
+            continue
+        key, _kernel, fetch_kib, write_kib = ln.rstrip("\n").split("\t")
+        out[key] = round((FETCH_FACTOR * float(fetch_kib) + WRITE_FACTOR * float(write_kib)) * 1024)
+    return out
 
 
 def build_cases(capi, stream, which):
@@ -88,7 +112,7 @@ def build_cases(capi, stream, which):
         fn, kern = linear_case(D(x), [D(w)], D(b), epi="GELU_TANH")
         flops = 2 * 128 * 768 * 3072
         cases["1"] = Case("GPT-2 c_fc Linear fp32 X[128,768] W[3072,768] +bias GELU-tanh", "TFLOP/s",
-                          flops / 1e12, "mfma", FP32_PEAK_TFLOPS, fn, kern, flops, 11415552, "f32")
+                          flops / 1e12, "mfma", FP32_PEAK_TFLOPS, fn, kern, flops, 11415552, "f32", "1")
 
     if "2" in which:   # decode GEMV, M in {1,4,8}; rotate W copies past the MALL
         w0 = f16(rng.standard_normal((2048, 8192)) * 0.02).T.copy()
@@ -99,7 +123,7 @@ def build_cases(capi, stream, which):
             fn, kern = linear_case(x, ws)
             byts = 2048 * 8192 * 2 + m * 2048 * 2 + m * 8192 * 4
             cases[f"2/M={m}"] = Case(f"decode GEMV M={m} K=2048 N=8192 fp16 W, fp32 acc/out", "GB/s",
-                                     byts / 1e9, "hbm", HBM_PEAK_GBS, fn, kern, 2 * m * 2048 * 8192, byts, "f16")
+                                     byts / 1e9, "hbm", HBM_PEAK_GBS, fn, kern, 2 * m * 2048 * 8192, byts, "f16", f"2/M={m}")
 
     if "3" in which:   # prefill gate/up, fused SiLU(g)*u
         wg = f16(rng.standard_normal((3072, 8192)) * 0.02).T
@@ -109,7 +133,7 @@ def build_cases(capi, stream, which):
         fn, kern = linear_case(x, [D(w)], gated=True)
         flops = 2 * 2048 * 3072 * 16384
         cases["3"] = Case("prefill gate/up X[2048,3072] W[2x8192,3072] fp16, SiLU(g)*u fused, fp32 out",
-                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn, kern, flops, 180355072, "f16")
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn, kern, flops, 180355072, "f16", "3")
 
     if "4" in which:   # attention scores; rotate S outputs past the MALL
         q = D(f16(rng.standard_normal((8, 1024, 256))))
@@ -123,7 +147,7 @@ def build_cases(capi, stream, which):
         fn4.keep = [q, k, outs, args]
         cases["4"] = Case("attention scores Q,K[8,1024,256] fp16, S=QK^T/16 fp32 causal", "GB/s",
                           41943040 / 1e9, "hbm", HBM_PEAK_GBS, fn4, "scores_kernel (128x128, DMA staging)", 2 * 8 * 1024 * 1024 * 256,
-                          41943040, "f16")
+                          41943040, "f16", "4")
 
     if "5" in which:   # YOLOX 3x3 conv, bias + SiLU
         wt = D(f16(rng.standard_normal((128, 128, 3, 3)) * 0.03))
@@ -142,7 +166,7 @@ def build_cases(capi, stream, which):
         fn5.keep = [wt, bias, x, out, a5, ws5]
         flops = 2 * 6400 * 128 * 1152
         cases["5"] = Case("YOLOX-s 3x3 conv in[1,128,80,80] W[128,128,3,3] fp16 +bias SiLU, fp32 out",
-                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn5, "conv_kernel<3> (implicit GEMM, packed weight)", flops, 5210368, "f16")
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn5, "conv_kernel<3> (implicit GEMM, packed weight)", flops, 5210368, "f16", "5")
     return cases
 
 
@@ -166,21 +190,41 @@ def time_case(capi, stream, case, steps, warmup, repeats):
 
 def cpu_baseline(budget_s):
     """The oracle's fp32 GEMV (the linear-slab contract) on the host, timed
-    on a bounded sample of config 2 (M=1): repeated full GEMVs for ~budget_s."""
+    on a bounded sample of config 2 (M=1): repeated full GEMVs for ~budget_s,
+    rotating over 6 copies of W (6 x 64 MiB fp32) so that the host's last-level
+    cache cannot serve W between calls, as HBM serves it on the GPU."""
     from oracle import oracle
     rng = np.random.default_rng(0)
-    w = f16(rng.standard_normal((8192, 2048)) * 0.02).astype(np.float32)
+    w0 = f16(rng.standard_normal((8192, 2048)) * 0.02).astype(np.float32)
+    ws = [w0.copy() for _ in range(6)]
     x = f16(rng.standard_normal((1, 2048))).astype(np.float32)
-    oracle.gemm_f32(x, w)
+    oracle.gemm_f32(x, ws[0])
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s:
-        oracle.gemm_f32(x, w)
+        oracle.gemm_f32(x, ws[n % len(ws)])
         n += 1
     dt = (time.perf_counter() - t0) / n
     byts = 2048 * 8192 * 2 + 2048 * 2 + 8192 * 4
     return {"value": round(byts / dt / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
             "sample": f"oracle fp32 GEMV (vai_oracle.c orc_gemm_f32) on config 2 M=1, W widened to fp32; "
-                      f"{n} calls in {budget_s:.0f}s, bytes counted as the fp16 problem's"}
+                      f"{n} calls in {budget_s:.0f}s rotating 6 W copies, bytes counted as the fp16 problem's"}
+
+
+def traffic_probe(capi, stream, cases, reps):
+    """Launches for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs: first the
+    calibration kernel (GatedMul over [4096, 4096] fp32 -> [4096, 2048]: reads
+    64 MiB, writes 32 MiB), then `reps` launches of every workload."""
+    gin = capi.DeviceArray((4096, 4096), np.float32)
+    gin.fill_(0)
+    gout = capi.DeviceArray((4096, 2048), np.float32)
+    for _ in range(5):
+        capi.gated_mul(gout, gin, "NONE", stream=stream.ptr)
+    stream.synchronize()
+    for key, case in cases.items():
+        for i in range(reps):
+            case.launch(i)
+        stream.synchronize()
+        print(f"# traffic probe: {key} x{reps}", file=sys.stderr, flush=True)
 
 
 def main():
@@ -194,6 +238,10 @@ def main():
     capi.check(capi.lib().vai_set_device(0), "set_device")
     stream = capi.Stream()
     cases = build_cases(capi, stream, set(args.configs.split(",")))
+    if args.traffic_probe:
+        traffic_probe(capi, stream, cases, args.traffic_probe)
+        return
+    traffic = load_traffic()
     report = {}
     for key, case in cases.items():
         ms = time_case(capi, stream, case, args.steps, args.warmup, args.repeats)
@@ -204,7 +252,7 @@ def main():
             "ms_per_step": round(ms, 6), "dtype": case.dtype,
             "roofline": {"bound": case.bound, "achieved": round(achieved, 3), "peak": case.peak,
                          "unit": "GB/s" if case.bound == "hbm" else "TFLOP/s",
-                         "frac": round(achieved / case.peak, 4), "traffic": None},
+                         "frac": round(achieved / case.peak, 4), "traffic": traffic.get(case.tkey)},
         }
         print(f"# cfg {key}: {case.name}: {ms*1e3:.2f} us/step, {rate:.1f} {case.unit}, "
               f"{100*achieved/case.peak:.1f}% of {case.bound} peak [{case.kernel}]", file=sys.stderr, flush=True)

@@ -23,6 +23,9 @@ COMMON = ["-O3", "-fPIC", "-std=c++20", f"--offload-arch={ARCH}", "-I", os.path.
 
 
 PYMOD_SRC = os.path.join(ENGINE, "pyvai.cpp")
+# C++ programs that use the engine the way a model does; the GPU tests run them.
+CPP_TESTS = os.path.join(ROOT, "tests", "cpp")
+CPP_TEST_BIN = os.path.join(CPP_TESTS, "_bin")
 
 
 def _sources():
@@ -82,7 +85,26 @@ def build(jobs=None):
         raise RuntimeError("link failed:\n" + r.stderr)
     os.replace(tmp, LIB)
     _build_pymodule()
+    _build_cpp_programs()
     return LIB
+
+
+def _build_cpp_programs():
+    """tests/cpp/*.cpp -> tests/cpp/_bin/<name>, linked to libvai_amd.so."""
+    if not os.path.isdir(CPP_TESTS):
+        return
+    os.makedirs(CPP_TEST_BIN, exist_ok=True)
+    for f in sorted(os.listdir(CPP_TESTS)):
+        if not f.endswith(".cpp"):
+            continue
+        out = os.path.join(CPP_TEST_BIN, f[:-4])
+        cmd = [HIPCC, "-x", "hip", "-O2", "-std=c++20", f"--offload-arch={ARCH}", "-I", os.path.join(ROOT, "include"),
+               "-I", ENGINE, os.path.join(CPP_TESTS, f), "-o", out + ".tmp", "-L", HERE, "-lvai_amd",
+               "-Wl,-rpath," + os.path.relpath(HERE, CPP_TEST_BIN).join(["$ORIGIN/", ""])]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"C++ program {f} failed to build:\n" + r.stderr)
+        os.replace(out + ".tmp", out)
 
 
 if __name__ == "__main__":

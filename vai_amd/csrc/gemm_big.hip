@@ -9,20 +9,29 @@
 //    flop are then half of what a 64x64 wave tile needs.
 //  * K advances in 64-wide stages through 2 LDS stages (64 KB each: a 256x64
 //    slab of A and of B). Global memory is copied straight into LDS
-//    (global_load_lds_dwordx4, no VGPR round trip) one stage ahead of the
-//    MFMAs. Each wave waits only for its own copies of the stage it is about
-//    to read (s_waitcnt vmcnt) and one s_barrier per stage makes the other
-//    waves' copies visible; no LDS fence is needed because the copies are the
-//    only writes. Measured on MI355X: 32-wide stages x 4 (more lookahead,
-//    twice the barriers) is ~3% slower; streaming B from L2 into VGPRs to
-//    halve LDS traffic is ~25% slower (L2->CU traffic doubles for B).
+//    (buffer_load ... lds, no VGPR round trip; rows past the operand read as
+//    zero) one stage ahead of the MFMAs. Each wave waits only for its own
+//    copies of the stage it is about to read (s_waitcnt vmcnt) and one
+//    s_barrier per stage makes the other waves' copies visible; no LDS fence
+//    is needed because the copies are the only writes. Measured on MI355X:
+//    32-wide stages x 4 (more lookahead, twice the barriers) is ~3% slower;
+//    streaming B from L2 into VGPRs to halve LDS traffic is ~25% slower (L2->CU
+//    traffic doubles for B).
 //  * Slab rows are CH 16-byte chunks; chunk c of row r is stored at
 //    chunk c ^ ((r / RPW) % CH), RPW = rows per 256-byte bank window. The 16
 //    lanes one LDS cycle serves (16 rows of a fragment, one chunk) then hit 16
 //    distinct 16-byte bank groups.
-//  * Workgroups are dispatched round-robin over the 8 XCDs. The launch index
-//    is remapped so that one XCD's resident workgroups share A and B slabs in
+//  * Persistent: at most one workgroup per CU, each walking its tiles as one
+//    stream of K stages. The next tile's first copies are in flight while a
+//    finished tile is written straight from the accumulators (two 128-byte
+//    row segments per store instruction, no LDS round trip), and those stores
+//    drain behind the next tile's MFMAs.
+//  * Workgroups are dispatched round-robin over the 8 XCDs. Tile indices are
+//    remapped so that one XCD's resident workgroups share A and B slabs in
 //    its L2 (8 M-tiles x 4 N-tiles per round at the config-3 shape).
+#include <algorithm>
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -110,106 +119,215 @@ __device__ __forceinline__ void store_gated4(const GemmParams& p, uint32_t row, 
     }
 }
 
+// The accumulators are read through this so that the register allocator
+// keeps them in AGPRs across the tile loop (a plain VALU use of an MFMA
+// result lets it move accumulators into VGPRs and spill).
+__device__ __forceinline__ float agpr_read(float a)
+{
+    float v;
+    asm("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+
 __device__ __forceinline__ void wait_lgkmcnt0()
 {
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
+// Tile order: launch-order index L -> (tm, tn). Workgroup b runs on XCD
+// b % 8 and handles L = b, b + G, ... (G % 8 == 0), so the tiles resident on
+// one XCD at a time (8 M-tiles x 4 N-tiles at the config-3 shape) share
+// their A and B slabs in that XCD's L2.
+struct TileOrder {
+    uint32_t tiles_m, tiles_n;
+    bool xcd;
+    __host__ __device__ __forceinline__ void of(uint32_t L, uint32_t& tm, uint32_t& tn) const
+    {
+        if (xcd) {
+            const uint32_t x = L % 8, local = L / 8;
+            tm = local % tiles_m;
+            tn = x * (tiles_n / 8) + local / tiles_m;
+        } else {
+            tm = L % tiles_m;
+            tn = L / tiles_m;
+        }
+    }
+};
+
+// Persistent: a grid of at most one workgroup per CU walks its tiles as one
+// continuous stream of K stages, so the copies of a tile's first stages are
+// in flight while the previous tile's accumulators are written out, and the
+// output stores drain behind the next tile's MFMAs.
 template <bool GATED, int BK, int STAGES>
 __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
 {
     using namespace big;
     typedef Cfg<BK, STAGES> C;
     constexpr int CH = C::CH, STAGE_BYTES = C::STAGE_BYTES, LOADS = C::LOADS, KS = BK / 16;
+    static_assert(4 * LOADS * 64 == 2 * BM * CH, "copies cover one stage");
     extern __shared__ half8 lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in an SGPR
     const int wm = wave >> 1, wn = wave & 1;
-
-    // XCD-aware tile order: launch index L runs on XCD L % 8.
-    const uint32_t tiles_m = (p.M + BM - 1) / BM;
-    const uint32_t tiles_n = gridDim.x / tiles_m;
-    uint32_t tm, tn;
-    {
-        const uint32_t L = blockIdx.x, total = gridDim.x;
-        if (total % 8 == 0 && tiles_m <= 8 && (8 % tiles_m) == 0 && tiles_n % 8 == 0) {
-            const uint32_t xcd = L % 8, local = L / 8;
-            tm = local % tiles_m;
-            tn = xcd * (tiles_n / 8) + local / tiles_m;
-        } else {
-            tm = L % tiles_m;
-            tn = L / tiles_m;
-        }
-    }
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t M = p.M, K = p.K;
 
-    // This lane's source for each of its LOADS copies per stage. Copy i of
-    // wave w fills LDS slots [(w*LOADS + i)*64, +64) of the stage: the first
-    // half of the copies cover the A slab, the second the B slab. Slot s of
-    // a slab holds row s/CH, physical chunk s%CH = logical chunk ^ swizzle.
-    const _Float16* src[LOADS];
+    TileOrder order;
+    order.tiles_m = (M + BM - 1) / BM;
+    order.tiles_n = GATED ? (p.H + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+    const uint32_t total = order.tiles_m * order.tiles_n, G = gridDim.x;
+    order.xcd = G % 8 == 0 && total % 8 == 0 && order.tiles_m <= 8 && 8 % order.tiles_m == 0 &&
+                order.tiles_n % 8 == 0;
+    const int ktiles = (int)(K / BK);
+    const int my_tiles = (int)((total - blockIdx.x + G - 1) / G);
+    const int S = my_tiles * ktiles;   // K stages this workgroup runs
+
+    // Copies: waves 0-1 fill the A slab of a stage, waves 2-3 the B slab; copy
+    // i of wave w fills slots [(w*LOADS + i)*64, +64). Slot s of a slab holds
+    // row s/CH, physical chunk s%CH = logical chunk ^ swizzle. The per-lane
+    // byte offsets do not depend on the tile: the tile and the stage enter as
+    // one wave-uniform offset. Rows past M (A) or past N / 2H (B) lie beyond
+    // the buffer's extent and read as zero; gated tail columns read rows whose
+    // outputs are never stored.
+    const bool is_b = wave >= 2;
+    uint32_t voff[LOADS];
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-        const int slot = (wave * LOADS + i) * 64 + lane;           // stage-wide slot
-        const bool is_b = slot >= BM * CH;
-        const int s = is_b ? slot - BM * CH : slot;
-        const int row = s / CH, pch = s % CH, ch = pch ^ ((row / C::RPW) % CH);
-        if (!is_b) {
-            const uint32_t gm = min(m0 + row, M - 1);               // tail rows: any valid row, never stored
-            src[i] = (const _Float16*)p.A + (size_t)gm * K + ch * 8;
-        } else {
-            uint32_t gn;
-            if constexpr (GATED) {
-                // logical column -> W row: wave column wn covers 64 output columns,
-                // fragments 0-1 their gate rows and 2-3 the matching up rows
-                const int w_n = row / 128, within = row % 128, fn = within / 32, j = within % 32;
-                const uint32_t jo = min(tn * (BN / 2) + w_n * 64 + (fn & 1) * 32 + j, p.H - 1);
-                gn = jo + (fn >= 2 ? p.H : 0u);
-            } else {
-                gn = min(n0 + row, p.N - 1);
-            }
-            src[i] = (const _Float16*)p.B + (size_t)gn * K + ch * 8;
+        const int slot = ((wave & 1) * LOADS + i) * 64 + lane;
+        const int row = slot / CH, pch = slot % CH, ch = pch ^ ((row / C::RPW) % CH);
+        uint32_t r = row;
+        if constexpr (GATED) {
+            // logical column -> W row: wave column w_n covers 64 output columns,
+            // fragments 0-1 their gate rows and 2-3 the matching up rows
+            const int w_n = row / 128, within = row % 128, fn = within / 32, j = within % 32;
+            const uint32_t jo = w_n * 64 + (fn & 1) * 32 + j;
+            r = is_b ? jo + (fn >= 2 ? p.H : 0u) : (uint32_t)row;
         }
+        voff[i] = (r * K + ch * 8) * 2;
     }
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(is_b ? p.B : p.A), (short)0, (int)((size_t)(is_b ? p.N : M) * K * 2), 0x00020000);
+    const uint32_t tile_rows_b = GATED ? BN / 2 : BN;   // W rows one N-tile advances by (gate half)
+
     LDS_AS char* lds_base = (LDS_AS char*)(LDS_AS void*)lds;
-    const int ktiles = (int)(K / BK);
-    // Copies stage kt into ring slot kt % STAGES. Past the last stage the
-    // source is clamped to it: the copy is harmless (its slot is never read
-    // again) and keeps the number of copies in flight fixed, so every wait
-    // below is a compile-time vmcnt.
-    auto issue = [&](int kt) {
-        const int ksrc = min(kt, ktiles - 1);
-        LDS_AS char* dst = lds_base + (kt % STAGES) * STAGE_BYTES + wave * LOADS * 1024;
+    // Copies stage g of the stream into ring slot g % STAGES. Past the last
+    // stage the source is clamped to it: the copy is harmless (its slot is
+    // never read again) and keeps the number of copies in flight fixed, so
+    // every wait below is a compile-time vmcnt.
+    auto issue = [&](int g) __attribute__((always_inline)) {
+        const int gs = min(g, S - 1);
+        const int r = gs / ktiles, kt = gs - r * ktiles;
+        uint32_t tm, tn;
+        order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
+        const uint32_t base = (is_b ? tn * tile_rows_b : tm * BM) * K * 2 + (uint32_t)kt * BK * 2;
+        LDS_AS char* dst = lds_base + (g % STAGES) * STAGE_BYTES + wave * LOADS * 1024;
 #pragma unroll
         for (int i = 0; i < LOADS; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(src[i] + (size_t)ksrc * BK), (LDS_AS void*)(dst + i * 1024),
-                                             16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)(dst + i * 1024), 16, (int)voff[i], (int)base, 0, 0);
     };
     const int fr = lane & 31, fk = lane >> 5;
-    // Fragment reads of one 16-wide k substep of a stage.
-    auto read_frags = [&](int kt, int ks, half8* af, half8* bf) {
-        const half8* a = (const half8*)(lds_base + (kt % STAGES) * STAGE_BYTES);
-        const half8* b = a + BM * CH;
-        const int ch = ks * 2 + fk;
+    // Fragment rows of one wave are fr + 32*i (+ 128*wave row): the swizzle
+    // term (row / RPW) % CH is the same for all of them, so each 16-wide k
+    // substep needs one LDS address per slot and the fragments sit at
+    // immediate offsets from it.
+    static_assert((32 / C::RPW) % CH == 0, "fragment rows share the swizzle");
+    const int swz = (fr / C::RPW) % CH;
+    auto read_frags = [&](int g, int ks, half8* af, half8* bf) __attribute__((always_inline)) {
+        const int ch = (ks * 2 + fk) ^ swz;
+        LDS_AS const char* a = lds_base + (g % STAGES) * STAGE_BYTES + ((wm * 128 + fr) * CH + ch) * 16;
+        LDS_AS const char* b = lds_base + (g % STAGES) * STAGE_BYTES + BM * CH * 16 + ((wn * 128 + fr) * CH + ch) * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = a[C::slot(wm * 128 + i * 32 + fr, ch)];
+        for (int i = 0; i < 4; ++i) af[i] = *(LDS_AS const half8*)(a + i * 32 * CH * 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[j] = b[C::slot(wn * 128 + j * 32 + fr, ch)];
+        for (int j = 0; j < 4; ++j) bf[j] = *(LDS_AS const half8*)(b + j * 32 * CH * 16);
     };
 
-    float16v acc[4][4];
+    // Writes a finished tile straight from the accumulators. D[i][j] of a
+    // 32x32 fragment sits in lane j + 32*((i/4)%2), register (i%4) + 4*(i/8):
+    // for each register a half-wave holds 32 consecutive columns of one row,
+    // so every store instruction writes two 128-byte row segments.
+    // A row bias for the tile's columns, loaded before its K loop so the
+    // loads are long complete when the epilogue reads them (a load still in
+    // flight at the epilogue would make the compiler wait for every copy).
+    // Gated: [0..1] gate bias of fragment columns 0-1, [2..3] the up bias.
+    auto load_col_bias = [&](int r, float (&cb)[4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) cb[j] = 0.f;
+        uint32_t tm, tn;
+        order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
+        if constexpr (GATED) {
+            const uint32_t H = p.H, col0 = tn * (BN / 2) + wn * 64 + fr;
+            if (p.bias) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (float16v)0.f;
-    // Half of a substep's 16 MFMAs: fragment rows i = 2h, 2h+1.
-    auto mfma_half = [&](const half8* af, const half8* bf, int h) {
+                for (int jj = 0; jj < 2; ++jj)
+                    if (col0 + jj * 32 < H) {
+                        cb[jj] = ld(p.bias, p.bias_dtype, col0 + jj * 32);
+                        cb[jj + 2] = ld(p.bias, p.bias_dtype, H + col0 + jj * 32);
+                    }
+            }
+        } else {
+            const uint32_t N = p.N, col0 = tn * BN + wn * 128 + fr;
+            if (p.bias && p.bias_repeat == N) {
 #pragma unroll
-        for (int i = 2 * h; i < 2 * h + 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    if (col0 + j * 32 < N) cb[j] = ld(p.bias, p.bias_dtype, col0 + j * 32);
+            }
+        }
+    };
+
+    auto write_tile = [&](int r, float16v (&acc)[4][4], const float (&cb)[4]) __attribute__((always_inline)) {
+        // agpr_read is opaque to the compiler's hazard checks: give the last
+        // MFMAs' results the wait states a VALU read of them needs.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        uint32_t tm, tn;
+        order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
+        const uint32_t row0 = tm * BM + wm * 128 + 4 * fk;
+        if constexpr (GATED) {
+            const uint32_t H = p.H, col0 = tn * (BN / 2) + wn * 64 + fr;
+            const uint32_t epi = p.epilogue;
+            const bool out16 = p.c_dtype == DT_F16;
+            static_for<4>([&](auto I) __attribute__((always_inline)) {
+                static_for<2>([&](auto JJ) __attribute__((always_inline)) {
+                    static_for<16>([&](auto R) __attribute__((always_inline)) {
+                        constexpr int i = I, jj = JJ, rr = R;
+                        const uint32_t row = row0 + i * 32 + (rr % 4) + 8 * (rr / 4), col = col0 + jj * 32;
+                        if (row < M && col < H) {
+                            const float v = epilogue(agpr_read(acc[i][jj][rr]) + cb[jj], epi) * (agpr_read(acc[i][jj + 2][rr]) + cb[jj + 2]);
+                            const size_t o = (size_t)row * H + col;
+                            if (out16) ((half_t*)p.C)[o] = (half_t)v;
+                            else __builtin_nontemporal_store(v, (float*)p.C + o);
+                        }
+                    });
+                    __builtin_amdgcn_sched_barrier(0);   // 16 outputs at a time: few live registers
+                });
+            });
+        } else {
+            const uint32_t N = p.N, col0 = tn * BN + wn * 128 + fr;
+            static_for<4>([&](auto I) __attribute__((always_inline)) {
+                static_for<4>([&](auto J) __attribute__((always_inline)) {
+                    constexpr int i = I, j = J;
+                    const uint32_t col = col0 + j * 32;
+                    if (col < N) {
+                        static_for<16>([&](auto R) __attribute__((always_inline)) {
+                            constexpr int rr = R;
+                            const uint32_t row = row0 + i * 32 + (rr % 4) + 8 * (rr / 4);
+                            if (row < M) {
+                                const size_t o = (size_t)row * N + col;
+                                // a bias other than one [N] row: read per element
+                                const float bb = (p.bias && p.bias_repeat != N)
+                                    ? ld(p.bias, p.bias_dtype, p.bias_repeat ? o % p.bias_repeat : o) : cb[j];
+                                const float res = p.residual
+                                    ? ld(p.residual, p.residual_dtype, p.residual_repeat ? o % p.residual_repeat : o) : 0.f;
+                                const float v = finish(agpr_read(acc[i][j][rr]) + bb, res, p.epilogue, p.residual_order, p.scalar_scale);
+                                if (p.c_dtype == DT_F16) ((half_t*)p.C)[o] = (half_t)v;
+                                else __builtin_nontemporal_store(v, (float*)p.C + o);
+                            }
+                        });
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            });
+        }
     };
 
     // Prologue: all STAGES slots in flight, then stage 0 landed everywhere.
@@ -220,89 +338,63 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
     half8 fa[2][4], fb[2][4];   // fragments of the current and the next 16-wide substep
     read_frags(0, 0, fa[0], fb[0]);
 
-    for (int kt = 0; kt + 1 < ktiles; ++kt) {
-        static_for<KS>([&](auto Q) __attribute__((always_inline)) {
-            constexpr int q = Q, cur = q & 1, nxt = cur ^ 1;
-            if constexpr (q + 1 < KS) {
-                // MFMAs on substep q while substep q + 1's fragments load.
-                read_frags(kt, q + 1, fa[nxt], fb[nxt]);
-                mfma_half(fa[cur], fb[cur], 0);
-                mfma_half(fa[cur], fb[cur], 1);
+    int g = 0;
+    for (int r = 0; r < my_tiles; ++r) {
+        float cb[4];
+        load_col_bias(r, cb);
+        float16v acc[4][4];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 LDS read
-                }
-                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-                __builtin_amdgcn_sched_barrier(0);   // substeps do not mix
-            } else {
-                // Last substep: half its MFMAs cover the stage barrier; after it
-                // slot kt is free for stage kt + STAGES and stage kt + 1 is read.
-                mfma_half(fa[cur], fb[cur], 0);
-                __builtin_amdgcn_sched_barrier(0);       // these MFMAs stay ahead of the barrier
-                wait_lgkmcnt0();                         // this wave's reads of slot kt are done
-                wait_vmcnt<(STAGES - 2) * LOADS>();      // its copies of stage kt + 1 have landed
-                __builtin_amdgcn_s_barrier();
-                issue(kt + STAGES);
-                read_frags(kt + 1, 0, fa[nxt], fb[nxt]);
-                mfma_half(fa[cur], fb[cur], 1);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-                    __builtin_amdgcn_sched_group_barrier(0x020, LOADS / 8, 1);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        });
-    }
-    // Last stage (KS is even, so its substep 0 fragments sit in fa[0]).
-    static_for<KS>([&](auto Q) __attribute__((always_inline)) {
-        constexpr int q = Q, cur = q & 1, nxt = cur ^ 1;
-        if constexpr (q + 1 < KS) read_frags(ktiles - 1, q + 1, fa[nxt], fb[nxt]);
-        mfma_half(fa[cur], fb[cur], 0);
-        mfma_half(fa[cur], fb[cur], 1);
-    });
-    wait_vmcnt<0>();   // the clamped copies must land before LDS is reused
+            for (int j = 0; j < 4; ++j) acc[i][j] = (float16v)0.f;
+        // Half of a substep's 16 MFMAs: fragment rows i = 2h, 2h+1.
+        auto mfma_half = [&](const half8* af, const half8* bf, int h) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 2 * h; i < 2 * h + 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        };
 
-    // Epilogue, staged through the now idle LDS one 32-row fragment band at a
-    // time: each wave writes its 32x128 band (row stride 132 floats, so the
-    // two half-waves' rows fall in different banks), then reads it back by
-    // rows and stores 16 bytes per lane. D[i][j] of a fragment sits in lane
-    // j + 32*((i/4)%2), register (i%4) + 4*(i/8).
-    __builtin_amdgcn_s_barrier();
-    constexpr int EPS = 132;
-    float* ep = (float*)(lds_base + wave * (32 * EPS * 4));
-    const uint32_t rbase = m0 + wm * 128;
-    static_for<4>([&](auto I) __attribute__((always_inline)) {
-        constexpr int i = I;
-        static_for<4>([&](auto J) __attribute__((always_inline)) {
-            static_for<16>([&](auto R) __attribute__((always_inline)) {
-                constexpr int j = J, r = R;
-                ep[(8 * (r / 4) + 4 * fk + (r % 4)) * EPS + j * 32 + fr] = acc[i][j][r];
+        for (int kt = 0; kt < ktiles; ++kt, ++g) {
+            static_for<KS>([&](auto Q) __attribute__((always_inline)) {
+                constexpr int q = Q, cur = q & 1, nxt = cur ^ 1;
+                if constexpr (q + 1 < KS) {
+                    // MFMAs on substep q while substep q + 1's fragments load.
+                    read_frags(g, q + 1, fa[nxt], fb[nxt]);
+                    mfma_half(fa[cur], fb[cur], 0);
+                    mfma_half(fa[cur], fb[cur], 1);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 LDS read
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+                    __builtin_amdgcn_sched_barrier(0);   // substeps do not mix
+                } else {
+                    // Last substep: half its MFMAs cover the stage barrier; after it
+                    // slot g is free for stage g + STAGES and stage g + 1 is read.
+                    mfma_half(fa[cur], fb[cur], 0);
+                    __builtin_amdgcn_sched_barrier(0);       // these MFMAs stay ahead of the barrier
+                    wait_lgkmcnt0();                         // this wave's reads of slot g are done
+                    wait_vmcnt<(STAGES - 2) * LOADS>();      // its copies of stage g + 1 have landed
+                    __builtin_amdgcn_s_barrier();
+                    issue(g + STAGES);
+                    read_frags(g + 1, 0, fa[nxt], fb[nxt]);
+                    mfma_half(fa[cur], fb[cur], 1);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                        __builtin_amdgcn_sched_group_barrier(0x020, LOADS / 8, 1);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             });
-        });
-        __builtin_amdgcn_wave_barrier();
-        if constexpr (GATED) {
-            const int c4 = (lane & 15) * 4;
-            const uint32_t jo = tn * (BN / 2) + wn * 64 + c4;
-            for (int rl = lane >> 4; rl < 32; rl += 4) {
-                const float4v g = *(const float4v*)(ep + rl * EPS + c4);
-                const float4v u = *(const float4v*)(ep + rl * EPS + 64 + c4);
-                const uint32_t row = rbase + i * 32 + rl;
-                if (row < M) store_gated4(p, row, jo, g, u);
-            }
-        } else {
-            const int c4 = (lane & 31) * 4;
-            const uint32_t col = n0 + wn * 128 + c4;
-            for (int rl = lane >> 5; rl < 32; rl += 2) {
-                const float4v v = *(const float4v*)(ep + rl * EPS + c4);
-                const uint32_t row = rbase + i * 32 + rl;
-                if (row < M) store_linear4(p, row, col, v);
-            }
         }
-        __builtin_amdgcn_wave_barrier();
-    });
+        write_tile(r, acc, cb);
+    }
+    wait_vmcnt<0>();   // the clamped copies land before the workgroup retires
 }
 
 #ifndef VAI_BIG_BK
@@ -314,8 +406,9 @@ constexpr int kBigBK = VAI_BIG_BK, kBigStages = VAI_BIG_STAGES;
 bool gemm_big_ok(const GemmParams& p, bool gated)
 {
     const uint32_t ncols = gated ? 2 * p.H : p.N;
+    // byte offsets into A and W are 32-bit buffer offsets
     return p.a_dtype == DT_F16 && p.b_dtype == DT_F16 && p.K % kBigBK == 0 && p.splits == 1 && p.batch == 1 &&
-           ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.B % 16 == 0) &&
+           (size_t)p.M * p.K * 2 < (1u << 31) && (size_t)ncols * p.K * 2 < (1u << 31) &&
            (size_t)((p.M + 255) / 256) * ((ncols + 255) / 256) >= 128;
 }
 
@@ -331,7 +424,18 @@ hipError_t gemm_big_launch(const GemmParams& p, bool gated, hipStream_t s)
         if (e != hipSuccess) return e;
         attr_set[gated] = true;
     }
-    hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(256), lds, s, p);
+    // one workgroup per CU at most (the kernel walks its tiles); the CU count
+    // is read once per device
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!cus[dev]) {
+        hipError_t e = hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+    }
+    const uint32_t tiles = tiles_m * tiles_n;
+    const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)cus[dev]);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, p);
     return hipGetLastError();
 }
 

@@ -87,12 +87,20 @@ def build_cases(capi, stream, which):
     rng = np.random.default_rng(0)
     cases = {}
 
-    def linear_case(x, ws, bias=None, epi="NONE", gated=False, odt=np.float32):
+    def linear_case(x, ws, bias=None, epi="NONE", gated=False, odt=np.float32, pack=False):
         N = ws[0].shape[0] // 2 if gated else ws[0].shape[0]
         out = capi.DeviceArray(x.shape[:-1] + (N,), odt)
         args = [capi.linear_args(out, x, w, bias, epi=epi, gated=gated, gate_epi="SILU") for w in ws]
-        need = capi.linear_workspace_size(args[0])
         keep = [out, x, ws, bias]
+        if pack:
+            # prefill weights are packed once, as the engine's Linear does at prepare
+            for a in args:
+                packed = capi.linear_pack_weight(a, stream.ptr)
+                if packed is not None:
+                    a.packed_weight = packed.ptr
+                    keep.append(packed)
+            stream.synchronize()
+        need = capi.linear_workspace_size(args[0])
         if need:
             wsp = capi.DeviceArray((need,), np.uint8)
             keep.append(wsp)
@@ -130,7 +138,7 @@ def build_cases(capi, stream, which):
         wu = f16(rng.standard_normal((3072, 8192)) * 0.02).T
         w = np.ascontiguousarray(np.concatenate([wg, wu], 0))
         x = D(f16(rng.standard_normal((2048, 3072))))
-        fn, kern = linear_case(x, [D(w)], gated=True)
+        fn, kern = linear_case(x, [D(w)], gated=True, pack=True)
         flops = 2 * 2048 * 3072 * 16384
         cases["3"] = Case("prefill gate/up X[2048,3072] W[2x8192,3072] fp16, SiLU(g)*u fused, fp32 out",
                           "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn, kern, flops, 180355072, "f16", "3")

@@ -85,10 +85,24 @@ typedef struct {
     uint32_t split_size;
     uint32_t gated;
     uint32_t gate_epilogue;
+    /* NULL, or vai_linear_pack_weight()'s output for this weight: prefill
+     * shapes (M > 8, fp16 I and W) then stream W into the matrix cores from
+     * that fragment-major copy instead of staging it through LDS. */
+    const void* packed_weight;
 } vai_linear_args;
 
 vai_status vai_linear_launch(const vai_linear_args* args, vai_stream_t stream);
 size_t vai_linear_workspace_size(const vai_linear_args* args);
+
+/* Size of, and the one-time fill of, the packed copy of args->weight that
+ * packed_weight takes (0 / VAI_ERR_UNSUPPORTED when the shape or dtypes have
+ * no packed path: fp16 I and W, K % 128 == 0, K >= 256). Depends on N, K,
+ * the dtypes and `gated`, not on M. The weight-side counterpart of the
+ * reference preparing a Linear's weights once at prepare time
+ * (/root/reference/vai/nodes/linear.h:2291-2704). */
+size_t vai_linear_packed_weight_size(const vai_linear_args* args);
+vai_status vai_linear_pack_weight(const vai_linear_args* args, void* packed, size_t packed_bytes,
+                                  vai_stream_t stream);
 
 /* Which kernel vai_linear_launch picks for args (for tests and reports):
  * writes a short name ("slab", "slab_scalar", "tile_f16_128x128", ...). */

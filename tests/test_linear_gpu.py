@@ -5,6 +5,8 @@ nodes/test_linear.py:11-84): slab M <= 8 at the FP32 tier, tile M > 8, odd N,
 split-K, K tails, residual before/after; then BASELINE's configs 1-3.
 Draws follow node_check: default_rng(0), params (weight, bias) before inputs.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -196,3 +198,57 @@ def test_linear_big_tile(gpu, m, k, n, gated, odt, epi, residual):
         want = oracle.linear(x[rows], w, b, r, epi=epi, out_dtype=odt, stage="tile")
     tol = FP16 if odt == np.float16 else TRANS
     assert_close(got[rows].astype(np.float32), want.astype(np.float32), tol)
+
+
+@pytest.mark.parametrize("m, k, n, gated, odt, epi, residual, bias", [
+    (1024, 512, 8192, False, np.float32, "GELU_TANH", True, True),    # residual [N]: per-output path
+    (1000, 384, 8200, False, np.float16, "RELU", False, True),        # M and N tails, fp16 out
+    (777, 256, 2 * 4160, True, np.float32, "SILU", False, True),      # gated, M and H tails
+    (2048, 512, 2 * 4096, True, np.float16, "GELU", False, False),
+    (2048, 768, 2 * 4096, True, np.float32, "GELU_TANH", False, True),
+    (4096, 256, 4096, False, np.float32, "NONE", False, False),       # full tiles, fast stores
+    (2304, 1280, 2 * 2048, True, np.float32, "SIGMOID", False, False),  # runtime-activation fast path
+])
+def test_linear_packed_weight(gpu, m, k, n, gated, odt, epi, residual, bias):
+    """The packed-weight prefill path (weight streamed into VGPRs in fragment
+    order) vs the oracle on sampled rows, through vai_linear_pack_weight."""
+    rng = np.random.default_rng(0)
+    w = draw(normal((n, k), 0.05), rng, np.float16)
+    b = draw(normal((n,), 0.05), rng, np.float16) if bias else None
+    x = draw((m, k), rng, np.float16)
+    r = draw((n,), rng, odt) if residual else None
+    kw = dict(gated=True, gate_epi=epi) if gated else dict(epi=epi)
+    D = gpu.DeviceArray.from_numpy
+    dx, dw = D(x), D(w)
+    out = gpu.DeviceArray((m, n // 2 if gated else n), odt)
+    a = gpu.linear_args(out, dx, dw, D(b) if bias else None, D(r) if residual else None, **kw)
+    packed = gpu.linear_pack_weight(a)
+    assert packed is not None
+    a.packed_weight = packed.ptr
+    assert gpu.linear_plan(a)[0].startswith("tile_f16_256x256_packed")
+    got = gpu.linear(out, dx, dw, D(b) if bias else None, D(r) if residual else None, packed=packed, **kw).numpy()
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(m - 4, m),
+                                     np.random.default_rng(1).choice(m, 24, replace=False)]))
+    if gated:
+        want = oracle.gated_mul(oracle.linear(x[rows], w, b, stage="tile"), epi=epi, out_dtype=odt)
+    else:
+        want = oracle.linear(x[rows], w, b, r, epi=epi, out_dtype=odt, stage="tile")
+    tol = FP16 if odt == np.float16 else TRANS
+    assert_close(got[rows].astype(np.float32), want.astype(np.float32), tol)
+    # same MFMA order as the LDS-staged kernel: bit-identical outputs
+    ref = run_linear(gpu, x, w, b, r, out_dtype=odt, **kw)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_linear_packed_weight_rejects(gpu):
+    """No packed path for fp32 weights or K % 128 != 0; a short buffer is refused."""
+    D = gpu.DeviceArray
+    a = gpu.linear_args(D((512, 512), np.float32), D((512, 384), np.float32), D((512, 384), np.float32))
+    assert gpu.lib().vai_linear_packed_weight_size(ctypes.byref(a)) == 0
+    a = gpu.linear_args(D((512, 512), np.float32), D((512, 320), np.float16), D((512, 320), np.float16))
+    assert gpu.lib().vai_linear_packed_weight_size(ctypes.byref(a)) == 0
+    a = gpu.linear_args(D((512, 512), np.float32), D((512, 384), np.float16), D((512, 384), np.float16))
+    n = gpu.lib().vai_linear_packed_weight_size(ctypes.byref(a))
+    assert n == 2 * 8 * 384 * 64
+    small = D((n - 16,), np.uint8)
+    assert gpu.lib().vai_linear_pack_weight(ctypes.byref(a), small.ptr, small.nbytes, None) == 1004

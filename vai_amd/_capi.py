@@ -19,6 +19,7 @@ RESIDUAL_ORDERS = {"AFTER_EPILOGUE": 0, "BEFORE_EPILOGUE": 1}
 # Every symbol include/vai_amd.h declares (checked by tests/test_capi_symbols.py).
 EXPORTS = [
     "vai_linear_launch", "vai_linear_workspace_size", "vai_linear_plan", "vai_gated_mul_launch",
+    "vai_linear_packed_weight_size", "vai_linear_pack_weight",
     "vai_conv2d_launch", "vai_conv2d_workspace_size", "vai_conv2d_packed_weight_size", "vai_conv2d_pack_weight",
     "vai_attn_scores_launch",
     "vai_device_count", "vai_set_device", "vai_malloc", "vai_free", "vai_memcpy_h2d", "vai_memcpy_d2h",
@@ -41,6 +42,7 @@ class LinearArgs(ctypes.Structure):
         ("bias_repeat", ctypes.c_uint32), ("residual_repeat", ctypes.c_uint32),
         ("scalar_scale", ctypes.c_float), ("split_size", ctypes.c_uint32),
         ("gated", ctypes.c_uint32), ("gate_epilogue", ctypes.c_uint32),
+        ("packed_weight", ctypes.c_void_p),
     ]
 
 
@@ -86,6 +88,9 @@ def lib():
         L.vai_linear_workspace_size.restype = sz
         L.vai_linear_plan.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_char_p, sz, ctypes.POINTER(u32)]
         L.vai_gated_mul_launch.argtypes = [vp, i32, vp, i32, u32, u32, u32, vp]
+        L.vai_linear_packed_weight_size.argtypes = [ctypes.POINTER(LinearArgs)]
+        L.vai_linear_packed_weight_size.restype = sz
+        L.vai_linear_pack_weight.argtypes = [ctypes.POINTER(LinearArgs), vp, sz, vp]
         L.vai_conv2d_launch.argtypes = [ctypes.POINTER(Conv2dArgs), vp]
         L.vai_conv2d_workspace_size.argtypes = [ctypes.POINTER(Conv2dArgs)]
         L.vai_conv2d_workspace_size.restype = sz
@@ -220,9 +225,23 @@ def linear_plan(args):
     return buf.value.decode(), n.value
 
 
-def linear(out, inp, weight, bias=None, residual=None, stream=None, **kw):
-    """Launches the Linear kernels; allocates the split-K workspace if needed."""
+def linear_pack_weight(args, stream=None):
+    """Packs args' weight once for the prefill path; returns the packed
+    buffer (None when the shape or dtypes have no packed path)."""
+    n = lib().vai_linear_packed_weight_size(ctypes.byref(args))
+    if not n:
+        return None
+    packed = DeviceArray((n,), np.uint8)
+    check(lib().vai_linear_pack_weight(ctypes.byref(args), packed.ptr, packed.nbytes, stream), "linear_pack_weight")
+    return packed
+
+
+def linear(out, inp, weight, bias=None, residual=None, stream=None, packed=None, **kw):
+    """Launches the Linear kernels; allocates the split-K workspace if needed.
+    packed: a linear_pack_weight() result for the weight (prefill shapes)."""
     a = linear_args(out, inp, weight, bias, residual, **kw)
+    if packed is not None:
+        a.packed_weight = packed.ptr
     ws = None
     need = linear_workspace_size(a)
     if need and a.workspace_bytes < need:

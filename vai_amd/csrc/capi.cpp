@@ -26,7 +26,7 @@ size_t dtype_bytes(int32_t d) { return d == VAI_DTYPE_F16 ? 2 : 4; }
 vai_status hip_status(hipError_t e) { return e == hipSuccess ? VAI_OK : (vai_status)e; }
 
 struct LinearPlan {
-    enum Kind { Slab, SlabThenGate, Tile, BigTile } kind;
+    enum Kind { Slab, SlabThenGate, Tile, BigTile, PackedTile } kind;
     GemmTile tile;
     uint32_t bm, bn;
     uint32_t split_size, splits;
@@ -74,6 +74,13 @@ LinearPlan plan_linear(const vai_linear_args* a)
         GemmParams g{};
         g.a_dtype = a->i_dtype; g.b_dtype = a->w_dtype; g.M = M; g.N = N; g.K = K; g.H = a->gated ? N / 2 : 0;
         g.A = a->in; g.B = a->weight; g.splits = 1; g.batch = 1;
+        if (a->split_size == 0 && a->packed_weight && gemm_packed_ok(g, a->gated)) {
+            p.kind = LinearPlan::PackedTile;
+            p.splits = 1;
+            p.split_size = K;
+            p.workspace = 0;
+            return p;
+        }
         if (a->split_size == 0 && gemm_big_ok(g, a->gated)) {
             p.kind = LinearPlan::BigTile;
             p.splits = 1;
@@ -149,8 +156,9 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
         sp.M = a->M;
         snprintf(buf, sizeof buf, "%s%s", (sp.M >= 2 && gemv_mfma_ok(sp)) ? "slab_mfma" : slab_vec_ok(sp) ? "slab" : "slab_scalar",
                  p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
-    } else if (p.kind == LinearPlan::BigTile) {
-        snprintf(buf, sizeof buf, "tile_f16_256x256%s", a->gated ? "_gated" : "");
+    } else if (p.kind == LinearPlan::BigTile || p.kind == LinearPlan::PackedTile) {
+        snprintf(buf, sizeof buf, "tile_f16_256x256%s%s", p.kind == LinearPlan::PackedTile ? "_packed" : "",
+                 a->gated ? "_gated" : "");
     } else {
         const bool f32 = a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32;
         snprintf(buf, sizeof buf, "tile_%s_%s%s", f32 ? "f32" : "f16", tile_name(p.tile, a->gated),
@@ -202,6 +210,7 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
     g.H = a->gated ? a->N / 2 : 0;
     if (p.splits > 1) { g.C = a->workspace; g.c_dtype = VAI_DTYPE_F32; }
     else { g.C = a->out; g.c_dtype = a->o_dtype; }
+    if (p.kind == LinearPlan::PackedTile) return hip_status(gemm_packed_launch(g, a->packed_weight, a->gated != 0, s));
     if (p.kind == LinearPlan::BigTile) return hip_status(gemm_big_launch(g, a->gated != 0, s));
     hipError_t e = gemm_launch(g, a->gated ? BKind::Gated : BKind::Dense,
                                a->gated ? EpiKind::Gated : EpiKind::Linear, p.tile, s);
@@ -211,6 +220,31 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
                                            a->bias, a->b_dtype, a->bias_repeat, a->residual, a->residual_repeat,
                                            a->epilogue, a->residual_order, a->scalar_scale,
                                            a->gated ? a->N / 2 : 0, a->gate_epilogue, a->N, s));
+}
+
+// The packed path needs fp16 I and W and K % 128 == 0, K >= 256 (two K
+// stages per loop trip, copies at most one tile ahead); the size does not
+// depend on M.
+static bool linear_packable(const vai_linear_args* a)
+{
+    return a && a->i_dtype == VAI_DTYPE_F16 && a->w_dtype == VAI_DTYPE_F16 && a->N > 0 && a->K >= 256 &&
+           a->K % 128 == 0 && (!a->gated || a->N % 2 == 0);
+}
+
+size_t vai_linear_packed_weight_size(const vai_linear_args* a)
+{
+    if (!linear_packable(a)) return 0;
+    return gemm_packed_weight_bytes(a->N, a->K, a->gated ? a->N / 2 : 0, a->gated != 0);
+}
+
+vai_status vai_linear_pack_weight(const vai_linear_args* a, void* packed, size_t packed_bytes, vai_stream_t stream)
+{
+    if (!a || !a->weight || !packed) return VAI_ERR_INVALID_ARG;
+    if (!linear_packable(a)) return VAI_ERR_UNSUPPORTED;
+    const size_t need = vai_linear_packed_weight_size(a);
+    if (packed_bytes < need) return VAI_ERR_WORKSPACE;
+    return hip_status(gemm_pack_weight(packed, a->weight, a->N, a->K, a->gated ? a->N / 2 : 0, a->gated != 0,
+                                       (hipStream_t)stream));
 }
 
 vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int32_t i_dtype, uint32_t rows,

@@ -34,6 +34,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "tile_store.h"
 
 #define LDS_AS __attribute__((address_space(3)))
 
@@ -119,40 +120,10 @@ __device__ __forceinline__ void store_gated4(const GemmParams& p, uint32_t row, 
     }
 }
 
-// The accumulators are read through this so that the register allocator
-// keeps them in AGPRs across the tile loop (a plain VALU use of an MFMA
-// result lets it move accumulators into VGPRs and spill).
-__device__ __forceinline__ float agpr_read(float a)
-{
-    float v;
-    asm("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
-    return v;
-}
-
 __device__ __forceinline__ void wait_lgkmcnt0()
 {
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
-
-// Tile order: launch-order index L -> (tm, tn). Workgroup b runs on XCD
-// b % 8 and handles L = b, b + G, ... (G % 8 == 0), so the tiles resident on
-// one XCD at a time (8 M-tiles x 4 N-tiles at the config-3 shape) share
-// their A and B slabs in that XCD's L2.
-struct TileOrder {
-    uint32_t tiles_m, tiles_n;
-    bool xcd;
-    __host__ __device__ __forceinline__ void of(uint32_t L, uint32_t& tm, uint32_t& tn) const
-    {
-        if (xcd) {
-            const uint32_t x = L % 8, local = L / 8;
-            tm = local % tiles_m;
-            tn = x * (tiles_n / 8) + local / tiles_m;
-        } else {
-            tm = L % tiles_m;
-            tn = L / tiles_m;
-        }
-    }
-};
 
 // Persistent: a grid of at most one workgroup per CU walks its tiles as one
 // continuous stream of K stages, so the copies of a tile's first stages are
@@ -171,12 +142,9 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
     const int wm = wave >> 1, wn = wave & 1;
     const uint32_t M = p.M, K = p.K;
 
-    TileOrder order;
-    order.tiles_m = (M + BM - 1) / BM;
-    order.tiles_n = GATED ? (p.H + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-    const uint32_t total = order.tiles_m * order.tiles_n, G = gridDim.x;
-    order.xcd = G % 8 == 0 && total % 8 == 0 && order.tiles_m <= 8 && 8 % order.tiles_m == 0 &&
-                order.tiles_n % 8 == 0;
+    const uint32_t G = gridDim.x;
+    const TileOrder order = TileOrder::make((M + BM - 1) / BM, GATED ? (p.H + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN, G);
+    const uint32_t total = order.tiles_m * order.tiles_n;
     const int ktiles = (int)(K / BK);
     const int my_tiles = (int)((total - blockIdx.x + G - 1) / G);
     const int S = my_tiles * ktiles;   // K stages this workgroup runs
@@ -204,8 +172,6 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
         }
         voff[i] = (r * K + ch * 8) * 2;
     }
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(is_b ? p.B : p.A), (short)0, (int)((size_t)(is_b ? p.N : M) * K * 2), 0x00020000);
     const uint32_t tile_rows_b = GATED ? BN / 2 : BN;   // W rows one N-tile advances by (gate half)
 
     LDS_AS char* lds_base = (LDS_AS char*)(LDS_AS void*)lds;
@@ -215,14 +181,24 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
     // every wait below is a compile-time vmcnt.
     auto issue = [&](int g) __attribute__((always_inline)) {
         const int gs = min(g, S - 1);
-        const int r = gs / ktiles, kt = gs - r * ktiles;
+        const int r = gs / ktiles;
+        const int kt = __builtin_amdgcn_readfirstlane(gs - r * ktiles);   // uniform (the divisions run on VALU)
         uint32_t tm, tn;
         order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
-        const uint32_t base = (is_b ? tn * tile_rows_b : tm * BM) * K * 2 + (uint32_t)kt * BK * 2;
+        tm = __builtin_amdgcn_readfirstlane(tm);
+        tn = __builtin_amdgcn_readfirstlane(tn);
+        // The resource starts at the tile's first row (of A, or of W) and ends
+        // at the operand's last row: rows past it are out of bounds (read as
+        // zero) through the per-lane offset alone.
+        const uint32_t row0 = is_b ? tn * tile_rows_b : tm * BM;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((const half_t*)(is_b ? p.B : p.A) + (size_t)row0 * K), (short)0,
+            (int)(((is_b ? p.N : M) - row0) * K * 2), 0x00020000);
         LDS_AS char* dst = lds_base + (g % STAGES) * STAGE_BYTES + wave * LOADS * 1024;
 #pragma unroll
         for (int i = 0; i < LOADS; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)(dst + i * 1024), 16, (int)voff[i], (int)base, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)(dst + i * 1024), 16, (int)voff[i],
+                                                     (int)((uint32_t)kt * BK * 2), 0, 0);
     };
     const int fr = lane & 31, fk = lane >> 5;
     // Fragment rows of one wave are fr + 32*i (+ 128*wave row): the swizzle
@@ -245,91 +221,6 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
     // 32x32 fragment sits in lane j + 32*((i/4)%2), register (i%4) + 4*(i/8):
     // for each register a half-wave holds 32 consecutive columns of one row,
     // so every store instruction writes two 128-byte row segments.
-    // A row bias for the tile's columns, loaded before its K loop so the
-    // loads are long complete when the epilogue reads them (a load still in
-    // flight at the epilogue would make the compiler wait for every copy).
-    // Gated: [0..1] gate bias of fragment columns 0-1, [2..3] the up bias.
-    auto load_col_bias = [&](int r, float (&cb)[4]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) cb[j] = 0.f;
-        uint32_t tm, tn;
-        order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
-        if constexpr (GATED) {
-            const uint32_t H = p.H, col0 = tn * (BN / 2) + wn * 64 + fr;
-            if (p.bias) {
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj)
-                    if (col0 + jj * 32 < H) {
-                        cb[jj] = ld(p.bias, p.bias_dtype, col0 + jj * 32);
-                        cb[jj + 2] = ld(p.bias, p.bias_dtype, H + col0 + jj * 32);
-                    }
-            }
-        } else {
-            const uint32_t N = p.N, col0 = tn * BN + wn * 128 + fr;
-            if (p.bias && p.bias_repeat == N) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (col0 + j * 32 < N) cb[j] = ld(p.bias, p.bias_dtype, col0 + j * 32);
-            }
-        }
-    };
-
-    auto write_tile = [&](int r, float16v (&acc)[4][4], const float (&cb)[4]) __attribute__((always_inline)) {
-        // agpr_read is opaque to the compiler's hazard checks: give the last
-        // MFMAs' results the wait states a VALU read of them needs.
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-        uint32_t tm, tn;
-        order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
-        const uint32_t row0 = tm * BM + wm * 128 + 4 * fk;
-        if constexpr (GATED) {
-            const uint32_t H = p.H, col0 = tn * (BN / 2) + wn * 64 + fr;
-            const uint32_t epi = p.epilogue;
-            const bool out16 = p.c_dtype == DT_F16;
-            static_for<4>([&](auto I) __attribute__((always_inline)) {
-                static_for<2>([&](auto JJ) __attribute__((always_inline)) {
-                    static_for<16>([&](auto R) __attribute__((always_inline)) {
-                        constexpr int i = I, jj = JJ, rr = R;
-                        const uint32_t row = row0 + i * 32 + (rr % 4) + 8 * (rr / 4), col = col0 + jj * 32;
-                        if (row < M && col < H) {
-                            const float v = epilogue(agpr_read(acc[i][jj][rr]) + cb[jj], epi) * (agpr_read(acc[i][jj + 2][rr]) + cb[jj + 2]);
-                            const size_t o = (size_t)row * H + col;
-                            if (out16) ((half_t*)p.C)[o] = (half_t)v;
-                            else __builtin_nontemporal_store(v, (float*)p.C + o);
-                        }
-                    });
-                    __builtin_amdgcn_sched_barrier(0);   // 16 outputs at a time: few live registers
-                });
-            });
-        } else {
-            const uint32_t N = p.N, col0 = tn * BN + wn * 128 + fr;
-            static_for<4>([&](auto I) __attribute__((always_inline)) {
-                static_for<4>([&](auto J) __attribute__((always_inline)) {
-                    constexpr int i = I, j = J;
-                    const uint32_t col = col0 + j * 32;
-                    if (col < N) {
-                        static_for<16>([&](auto R) __attribute__((always_inline)) {
-                            constexpr int rr = R;
-                            const uint32_t row = row0 + i * 32 + (rr % 4) + 8 * (rr / 4);
-                            if (row < M) {
-                                const size_t o = (size_t)row * N + col;
-                                // a bias other than one [N] row: read per element
-                                const float bb = (p.bias && p.bias_repeat != N)
-                                    ? ld(p.bias, p.bias_dtype, p.bias_repeat ? o % p.bias_repeat : o) : cb[j];
-                                const float res = p.residual
-                                    ? ld(p.residual, p.residual_dtype, p.residual_repeat ? o % p.residual_repeat : o) : 0.f;
-                                const float v = finish(agpr_read(acc[i][j][rr]) + bb, res, p.epilogue, p.residual_order, p.scalar_scale);
-                                if (p.c_dtype == DT_F16) ((half_t*)p.C)[o] = (half_t)v;
-                                else __builtin_nontemporal_store(v, (float*)p.C + o);
-                            }
-                        });
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                });
-            });
-        }
-    };
-
     // Prologue: all STAGES slots in flight, then stage 0 landed everywhere.
 #pragma unroll
     for (int st = 0; st < STAGES; ++st) issue(st);
@@ -341,7 +232,11 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
     int g = 0;
     for (int r = 0; r < my_tiles; ++r) {
         float cb[4];
-        load_col_bias(r, cb);
+        {
+            uint32_t tm, tn;
+            order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
+            tile_col_bias<GATED>(p, tn, wn, fr, cb);
+        }
         float16v acc[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -392,7 +287,11 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
                 }
             });
         }
-        write_tile(r, acc, cb);
+        {
+            uint32_t tm, tn;
+            order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
+            tile_store<GATED>(p, acc, cb, tm, tn, wm, wn, fr, fk);
+        }
     }
     wait_vmcnt<0>();   // the clamped copies land before the workgroup retires
 }

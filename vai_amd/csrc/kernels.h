@@ -79,6 +79,13 @@ hipError_t gemm_launch(const GemmParams& p, BKind bk, EpiKind ek, GemmTile tile,
 bool gemm_big_ok(const GemmParams& p, bool gated);
 hipError_t gemm_big_launch(const GemmParams& p, bool gated, hipStream_t s);
 
+// The same shapes with a pre-packed fp16 weight (K % 128 == 0): the weight
+// streams into VGPRs in fragment order and only A goes through LDS.
+bool gemm_packed_ok(const GemmParams& p, bool gated);
+size_t gemm_packed_weight_bytes(uint32_t N, uint32_t K, uint32_t H, bool gated);
+hipError_t gemm_pack_weight(void* dst, const void* w, uint32_t N, uint32_t K, uint32_t H, bool gated, hipStream_t s);
+hipError_t gemm_packed_launch(const GemmParams& p, const void* packed, bool gated, hipStream_t s);
+
 // Attention scores for fp16 Q/K with head_dim % 64 == 0.
 bool scores_fast_ok(const GemmParams& p);
 hipError_t scores_launch(const GemmParams& p, hipStream_t s);

@@ -68,6 +68,7 @@ vai_linear_args Linear::args(bool withPointers) const
         const Tensor& part = (*this)["partial"];
         a.workspace = ptrOrNull(part);
         a.workspace_bytes = part.validShape() ? part.numBytes() : 0;
+        a.packed_weight = packedMatches(a) ? packed_.ptr() : nullptr;
     } else {
         // placeholders so argument checks see non-null operands
         a.in = a.weight = a.out = reinterpret_cast<void*>(256);
@@ -75,6 +76,11 @@ vai_linear_args Linear::args(bool withPointers) const
         a.residual = config_.acceptResidual ? reinterpret_cast<void*>(256) : nullptr;
     }
     return a;
+}
+
+bool Linear::packedMatches(const vai_linear_args& a) const
+{
+    return packed_ && packedFrom_ == (*this)["weight"].devicePtr() && packedGated_ == (a.gated != 0);
 }
 
 bool Linear::canFuseGate(const GatedMul& gm) const
@@ -113,6 +119,20 @@ void Linear::prepare()
     (*this)["out0"] = Tensor(shape, outputDtype());
 
     vai_linear_args a = args(false);
+    // Prefill shapes (M > 8) stream a fragment-major copy of the weight into
+    // the matrix cores; it is made once per weight buffer and layout (a fused
+    // gate changes the layout), as the reference prepares its weights once.
+    const size_t pbytes = M_ > 8 ? vai_linear_packed_weight_size(&a) : 0;
+    if (pbytes && (packedFrom_ != w.devicePtr() || packedGated_ != (a.gated != 0))) {
+        packed_ = bufferPool().requestBuffer(pbytes);
+        vai_linear_args pa = a;
+        pa.weight = w.devicePtr();
+        check(vai_linear_pack_weight(&pa, packed_.ptr(), packed_.size(), (vai_stream_t)net().stream()), "Linear");
+        check(vai_stream_sync((vai_stream_t)net().stream()), "Linear");
+        packedFrom_ = w.devicePtr();
+        packedGated_ = a.gated != 0;
+    }
+    a.packed_weight = packedMatches(a) ? packed_.ptr() : nullptr;
     char name[64] = {0};
     check(vai_linear_plan(&a, name, sizeof name, &splitCount_), "Linear");
     plan_ = name;

@@ -68,10 +68,14 @@ public:
 private:
     Dtype accDtype_ = Dtype::None;
     GatedMul* fused_ = nullptr;
+    PooledBuffer packed_;              // fragment-major copy of the weight for prefill shapes
+    const void* packedFrom_ = nullptr;
+    bool packedGated_ = false;
     uint32_t M_ = 0, biasRepeat_ = 0, residualRepeat_ = 0;
     std::string plan_;
     uint32_t splitCount_ = 1;
     vai_linear_args args(bool withPointers) const;
+    bool packedMatches(const vai_linear_args& a) const;
 };
 
 class GatedMul : public Node

@@ -14,19 +14,25 @@
 //     packed[lb][kc][r][0..7] = W[src_row(lb, r)][kc*8 .. kc*8+7]
 //
 // so one wave's fragment of one 16-wide k substep (32 rows x 2 chunks) is
-// 1 KB of contiguous memory: lane l reads bytes l*16 .. l*16+15. Logical
-// columns follow the tile layout of tile_store.h (for gated weights each
-// 128-column group is 64 gate rows then the 64 matching up rows); blocks past
+// 1 KB of contiguous memory: lane l reads bytes l*16 .. l*16+15. Blocks past
 // N (or H) are zero.
+//
+// Wave layout 1 x 4: wave w owns all 256 rows of the tile and logical
+// columns w*64 .. w*64+63 (8 x 2 fragments of 32x32, 256 fp32 accumulators
+// per lane in AGPRs). No wave loads what another loads, and every wave reads
+// all eight A fragments of a substep from LDS. For gated weights a wave's two
+// column fragments are the 32 gate rows and the 32 matching up rows of its
+// 32 outputs.
 //
 // Schedule (per workgroup, 4 waves, one workgroup per CU, persistent):
 //  * A: 256x64 fp16 stages (32 KB) copied global -> LDS (buffer_load ... lds)
 //    into a ring of 3 slots, two stages ahead; swizzled like gemm_big.hip.
-//  * B: each wave loads its 128 columns x 64 k (16 KB) of stage g + 1 into
-//    VGPRs at the start of stage g (16 x 1 KB loads), double buffered.
-//  * Per stage and wave: 64 MFMAs, 16 LDS fragment reads, 8 LDS copies, 16
+//  * B: each wave loads its 64 columns x 64 k (8 KB) of stage g + 1 into
+//    VGPRs during stage g (8 x 1 KB loads), double buffered.
+//  * Per stage and wave: 64 MFMAs, 32 LDS fragment reads, 8 LDS copies, 8
 //    global loads; one s_barrier per stage.
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -43,20 +49,22 @@ constexpr int RPW = 16 / CH;               // slab rows per 256-byte LDS bank wi
 constexpr int SLOTS = 3;                   // A ring depth
 constexpr int A_STAGE = BM * BK * 2;       // 32 KB
 constexpr int A_LOADS = A_STAGE / (4 * 1024);   // 1 KB copies per wave per stage
-constexpr int B_LOADS = 16;                // 16-byte fragment loads per lane per stage
+constexpr int B_LOADS = 8;                 // 16-byte fragment loads per lane per stage
 constexpr size_t LDS_BYTES = (size_t)SLOTS * A_STAGE;
 }
 
-// W row of logical block lb, row r (>= the row count when the block is padding).
+// W row of logical block lb, row r (0xFFFFFFFF when the block row is padding).
 __host__ __device__ inline uint32_t packed_src_row(uint32_t lb, uint32_t r, bool gated, uint32_t H, uint32_t N)
 {
     if (!gated) {
         const uint32_t row = lb * 32 + r;
         return row < N ? row : 0xFFFFFFFFu;
     }
-    const uint32_t t = lb / 8, w = (lb / 4) % 2, j = lb % 4;
-    const uint32_t jo = t * 128 + w * 64 + (j & 1) * 32 + r;
-    return jo < H ? jo + (j >= 2 ? H : 0u) : 0xFFFFFFFFu;
+    // tile t = lb / 8 covers outputs t*128.., wave w = (lb / 2) % 4 outputs
+    // t*128 + w*32.., block lb % 2: 0 = gate rows, 1 = up rows
+    const uint32_t t = lb / 8, w = (lb / 2) % 4, j = lb % 2;
+    const uint32_t jo = t * 128 + w * 32 + r;
+    return jo < H ? jo + (j ? H : 0u) : 0xFFFFFFFFu;
 }
 
 __host__ __device__ inline uint32_t packed_blocks(uint32_t N, uint32_t H, bool gated)
@@ -108,6 +116,135 @@ __device__ __forceinline__ void pk_wait_lgkmcnt0()
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
+// ---- epilogue for the 1 x 4 layout ----------------------------------------
+// D[i][j] of a 32x32 fragment sits in lane j + 32*((i/4)%2), register
+// (i%4) + 4*(i/8): per register a half-wave holds 32 consecutive columns of
+// one row. Row of fragment i, register rr: i*32 + (rr%4) + 8*(rr/4) + 4*fk.
+
+// Bias of this lane's columns, loaded before the tile's K loop (a load still
+// in flight at the epilogue would make the compiler wait for every copy
+// issued after it). Gated: [0] gate bias, [1] up bias of the lane's output.
+template <bool GATED>
+__device__ __forceinline__ void pk_col_bias(const GemmParams& p, uint32_t tn, int w, int fr, float (&cb)[2])
+{
+    cb[0] = cb[1] = 0.f;
+    if constexpr (GATED) {
+        const uint32_t H = p.H, col = tn * 128 + w * 32 + fr;
+        if (p.bias && col < H) {
+            cb[0] = ld(p.bias, p.bias_dtype, col);
+            cb[1] = ld(p.bias, p.bias_dtype, H + col);
+        }
+    } else {
+        const uint32_t N = p.N, col0 = tn * 256 + w * 64 + fr;
+        if (p.bias && p.bias_repeat == N) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (col0 + j * 32 < N) cb[j] = ld(p.bias, p.bias_dtype, col0 + j * 32);
+        }
+    }
+}
+
+// Fast path (fp32 output, the tile's columns inside the output, the bias one
+// row): buffer stores from a resource that starts at the tile's first row and
+// ends at the output's last row, so rows past M are dropped by the bounds
+// check; the common activations are compile-time (6 = the runtime kind).
+template <bool GATED, uint32_t EPI>
+__device__ __forceinline__ void pk_store_fast(const GemmParams& p, float16v (&acc)[8][2], const float (&cb)[2],
+                                              uint32_t tm, uint32_t tn, int w, int fr, int fk)
+{
+    const uint32_t ld_out = GATED ? p.H : p.N;
+    const uint32_t rows_left = p.M - tm * 256;
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((float*)p.C + (size_t)tm * 256 * ld_out), (short)0,
+        (int)std::min<size_t>((size_t)rows_left * ld_out * 4, 0x7FFFFFFF), 0x00020000);
+    const uint32_t col0 = GATED ? tn * 128 + w * 32 + fr : tn * 256 + w * 64 + fr;
+    const uint32_t lane_off = (4 * fk * ld_out + col0) * 4;
+    const uint32_t row_bytes = ld_out * 4;
+    const uint32_t epi = p.epilogue;
+    const float s = p.scalar_scale;
+    constexpr int JN = GATED ? 1 : 2;
+    static_for<8>([&](auto I) __attribute__((always_inline)) {
+        static_for<JN>([&](auto J) __attribute__((always_inline)) {
+            constexpr int i = I, j = J;
+            static_for<16>([&](auto R) __attribute__((always_inline)) {
+                constexpr int rr = R;
+                float v;
+                if constexpr (GATED)
+                    v = act<EPI>(agpr_read(acc[i][0][rr]) + cb[0], epi) * (agpr_read(acc[i][1][rr]) + cb[1]);
+                else
+                    v = s * act<EPI>(agpr_read(acc[i][j][rr]) + cb[j], epi);
+                const uint32_t voff = lane_off + (uint32_t)(i * 32 + (rr % 4) + 8 * (rr / 4)) * row_bytes + j * 128;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out, (int)voff, 0, 0);
+            });
+            __builtin_amdgcn_sched_barrier(0);   // 16 outputs at a time: few live registers
+        });
+    });
+}
+
+template <bool GATED>
+__device__ __forceinline__ void pk_store_any(const GemmParams& p, float16v (&acc)[8][2], const float (&cb)[2],
+                                             uint32_t tm, uint32_t tn, int w, int fr, int fk)
+{
+    const uint32_t M = p.M, row0 = tm * 256 + 4 * fk;
+    if constexpr (GATED) {
+        const uint32_t H = p.H, col = tn * 128 + w * 32 + fr;
+        static_for<8>([&](auto I) __attribute__((always_inline)) {
+            static_for<16>([&](auto R) __attribute__((always_inline)) {
+                constexpr int i = I, rr = R;
+                const uint32_t row = row0 + i * 32 + (rr % 4) + 8 * (rr / 4);
+                const float g = agpr_read(acc[i][0][rr]), u = agpr_read(acc[i][1][rr]);
+                if (row < M && col < H)
+                    st(p.C, p.c_dtype, (size_t)row * H + col, epilogue(g + cb[0], p.epilogue) * (u + cb[1]));
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    } else {
+        const uint32_t N = p.N, col0 = tn * 256 + w * 64 + fr;
+        static_for<8>([&](auto I) __attribute__((always_inline)) {
+            static_for<2>([&](auto J) __attribute__((always_inline)) {
+                constexpr int i = I, j = J;
+                const uint32_t col = col0 + j * 32;
+                static_for<16>([&](auto R) __attribute__((always_inline)) {
+                    constexpr int rr = R;
+                    const uint32_t row = row0 + i * 32 + (rr % 4) + 8 * (rr / 4);
+                    const float a = agpr_read(acc[i][j][rr]);
+                    if (row < M && col < N) {
+                        const size_t o = (size_t)row * N + col;
+                        // a bias other than one [N] row: read per element
+                        const float bb = (p.bias && p.bias_repeat != N)
+                            ? ld(p.bias, p.bias_dtype, p.bias_repeat ? o % p.bias_repeat : o) : cb[j];
+                        const float res = p.residual
+                            ? ld(p.residual, p.residual_dtype, p.residual_repeat ? o % p.residual_repeat : o) : 0.f;
+                        st(p.C, p.c_dtype, o, finish(a + bb, res, p.epilogue, p.residual_order, p.scalar_scale));
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+    }
+}
+
+template <bool GATED>
+__device__ __forceinline__ void pk_store(const GemmParams& p, float16v (&acc)[8][2], const float (&cb)[2],
+                                         uint32_t tm, uint32_t tn, int w, int fr, int fk)
+{
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");   // MFMA result -> VALU read distance
+    const bool cols_in = GATED ? tn * 128 + 128 <= p.H : tn * 256 + 256 <= p.N;
+    const bool plain = GATED || (!p.residual && (!p.bias || p.bias_repeat == p.N));   // cb holds the bias
+    if (cols_in && plain && p.c_dtype == DT_F32) {
+        switch (p.epilogue) {
+        case 4: pk_store_fast<GATED, 4>(p, acc, cb, tm, tn, w, fr, fk); break;   // SiLU
+        case 3: pk_store_fast<GATED, 3>(p, acc, cb, tm, tn, w, fr, fk); break;   // GELU-tanh
+        case 0: pk_store_fast<GATED, 0>(p, acc, cb, tm, tn, w, fr, fk); break;
+        default: pk_store_fast<GATED, 6>(p, acc, cb, tm, tn, w, fr, fk); break;
+        }
+    } else {
+        pk_store_any<GATED>(p, acc, cb, tm, tn, w, fr, fk);
+    }
+}
+
+// ---- the kernel ------------------------------------------------------------
 template <bool GATED>
 __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const half_t* __restrict__ wp)
 {
@@ -115,12 +252,11 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
     extern __shared__ half8 lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
     const int fr = lane & 31, fk = lane >> 5;
     const uint32_t M = p.M, K = p.K, G = gridDim.x;
     const TileOrder order = TileOrder::make((M + BM - 1) / BM, GATED ? (p.H + 127) / 128 : (p.N + BN - 1) / BN, G);
     const uint32_t total = order.tiles_m * order.tiles_n;
-    const int ktiles = (int)(K / BK);                      // even: the stage loop is unrolled by two
+    const int ktiles = (int)(K / BK);   // even, >= 4
     // (a division expands to VALU code: read it back as the scalar it is)
     const int my_tiles = __builtin_amdgcn_readfirstlane((int)((total - blockIdx.x + G - 1) / G));
 
@@ -128,6 +264,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
     // stages a workgroup runs are its tiles' K steps back to back; copies past
     // the last stage repeat it (harmless, and the copy counts stay fixed).
     struct Pos { uint32_t tm, tn; int kt; };
+
     // A copies: copy i of wave w fills slab slots [(w*A_LOADS + i)*64, +64);
     // slot s holds row s/CH, physical chunk s%CH = logical chunk ^ swizzle.
     uint32_t voff[A_LOADS];
@@ -140,9 +277,6 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
     LDS_AS char* lds_base = (LDS_AS char*)(LDS_AS void*)lds;
 
     auto issue_a = [&](int g, Pos at) __attribute__((always_inline)) {
-#ifdef PK_NO_A
-        if (g >= SLOTS) return;
-#endif
         // The resource starts at the tile's first row and ends at A's last
         // row: rows past M are out of bounds (read as zero) through the
         // per-lane offset alone, whatever the scalar offset does.
@@ -155,44 +289,40 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
                                                      (int)(at.kt * BK * 2), 0, 0);
     };
 
-    // A fragments of substep ks of stage g: rows wm*128 + i*32 + fr share the
-    // swizzle term, so the four fragments sit at immediate offsets.
+    // A fragments of substep ks of stage g: rows i*32 + fr share the swizzle
+    // term, so the eight fragments sit at immediate offsets.
     static_assert((32 / RPW) % CH == 0, "fragment rows share the swizzle");
     const int swz = (fr / RPW) % CH;
-    auto read_a = [&](int g, int ks, half8* af) __attribute__((always_inline)) {
-#ifdef PK_NO_LDSREAD
-        if (g > 0) return;
-#endif
+    auto read_a = [&](int g, int ks, half8 (&af)[8]) __attribute__((always_inline)) {
         const int ch = (ks * 2 + fk) ^ swz;
-        LDS_AS const char* a = lds_base + (g % SLOTS) * A_STAGE + ((wm * 128 + fr) * CH + ch) * 16;
+        LDS_AS const char* a = lds_base + (g % SLOTS) * A_STAGE + (fr * CH + ch) * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *(LDS_AS const half8*)(a + i * 32 * CH * 16);
+        for (int i = 0; i < 8; ++i) af[i] = *(LDS_AS const half8*)(a + i * 32 * CH * 16);
     };
 
-    // B fragments of stage g: fragment (q, j) is 1 KB at block tn*8 + wn*4 + j,
-    // chunk kt*8 + 2q; lane l reads its 16 bytes at l*16.
+    // B fragments of stage `at`, substep q: fragment j is 1 KB at block
+    // tn*8 + wave*2 + j, chunk kt*8 + 2q; lane l reads its 16 bytes at l*16.
     const size_t blk = (size_t)K * 64;
-    auto load_b = [&](Pos at, half8 (&fb)[4][4], int q) __attribute__((always_inline)) {
-        const char* base =
-            (const char*)wp + (size_t)(at.tn * 8 + wn * 4) * blk + (size_t)at.kt * 4096 + q * 1024 + lane * 16;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) fb[q][j] = *(const half8*)(base + j * blk);
-    };
 
-    auto mfma_rows = [&](float16v (&acc)[4][4], const half8* af, const half8 (&bq)[4], int i0, int i1)
+    auto mfma_rows = [&](float16v (&acc)[8][2], const half8 (&af)[8], const half8 (&bq)[2], int i0, int i1)
         __attribute__((always_inline)) {
 #pragma unroll
         for (int i = i0; i < i1; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 2; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bq[j], acc[i][j], 0, 0, 0);
     };
 
-    half8 fa[2][4];
-    half8 fb0[4][4], fb1[4][4];
+    half8 fa[2][8];
+    half8 fb0[4][2], fb1[4][2];
 
-    // One stage: MFMAs on (fa, cur) while the next stage's B loads into nxt
-    // and the next substep's A fragments come out of LDS.
+    auto load_b = [&](struct Pos at, half8 (&fb)[4][2], int q) __attribute__((always_inline)) {
+        const char* base =
+            (const char*)wp + (size_t)(at.tn * 8 + wave * 2) * blk + (size_t)at.kt * 4096 + q * 1024 + lane * 16;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fb[q][j] = *(const half8*)(base + j * blk);
+    };
+
     // Position d stages after K step kt of the current tile.
     auto ahead = [&](Pos here, Pos next, bool has_next, int d) __attribute__((always_inline)) {
         Pos at = here;
@@ -204,48 +334,45 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         return at;
     };
 
-    auto stage = [&](int g, Pos here, Pos next, bool has_next, float16v (&acc)[4][4], half8 (&cur)[4][4],
-                     half8 (&nxt)[4][4]) __attribute__((always_inline)) {
+    // One stage: MFMAs on (fa, cur) while the next stage's B loads into nxt
+    // and the next substep's A fragments come out of LDS.
+    auto stage = [&](int g, Pos here, Pos next, bool has_next, float16v (&acc)[8][2], half8 (&cur)[4][2],
+                     half8 (&nxt)[4][2]) __attribute__((always_inline)) {
         const Pos b_at = ahead(here, next, has_next, 1);
         static_for<4>([&](auto Q) __attribute__((always_inline)) {
             constexpr int q = Q, c = q & 1, n = c ^ 1;
             if constexpr (q < 3) {
-#ifndef PK_NO_B
                 load_b(b_at, nxt, q);
-#endif
                 read_a(g, q + 1, fa[n]);
-                mfma_rows(acc, fa[c], cur[q], 0, 4);
+                mfma_rows(acc, fa[c], cur[q], 0, 8);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < 8; ++u) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load (B)
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read (A)
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (u < 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load (B)
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
                 __builtin_amdgcn_sched_barrier(0);
             } else {
-#ifndef PK_NO_B
                 load_b(b_at, nxt, q);
-#endif
-                mfma_rows(acc, fa[c], cur[q], 0, 2);
+                mfma_rows(acc, fa[c], cur[q], 0, 4);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < 2; ++u) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
                 }
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 pk_wait_lgkmcnt0();                              // this wave's reads of slot g are done
                 pk_wait_vmcnt<A_LOADS + 2 * B_LOADS>();          // A(g+1) landed: B(g), A(g+2), B(g+1) may not
                 __builtin_amdgcn_s_barrier();
                 issue_a(g + SLOTS, ahead(here, next, has_next, SLOTS));
                 read_a(g + 1, 0, fa[n]);
-                mfma_rows(acc, fa[c], cur[q], 2, 4);
+                mfma_rows(acc, fa[c], cur[q], 4, 8);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < 8; ++u) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-                    __builtin_amdgcn_sched_group_barrier(0x020, 2, 1);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -261,20 +388,15 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         return Pos{(uint32_t)__builtin_amdgcn_readfirstlane(tm), (uint32_t)__builtin_amdgcn_readfirstlane(tn), 0};
     };
 
-    // Prologue: A stages 0..2 and B stage 0 of the first tile in flight
-    // (ktiles >= 4); wait for A(0).
-    // The issue order A(0), A(1), B(0), A(2) is the order the loop keeps
-    // (A(g+1), B(g), A(g+2) are the youngest copies at the top of stage g),
-    // so the compiler's waits for B registers come out the same on entry and
-    // on the back edge.
+    // Prologue. The issue order A(0), A(1), B(0), A(2) is the order the loop
+    // keeps (A(g+1), B(g), A(g+2) are the youngest copies at the top of stage
+    // g), so the compiler's waits for B registers come out the same on entry
+    // and on the back edge.
     Pos here = tile_pos(0);
     issue_a(0, Pos{here.tm, here.tn, 0});
     issue_a(1, Pos{here.tm, here.tn, 1});
 #pragma unroll
     for (int q = 0; q < 4; ++q) load_b(here, fb0, q);
-#ifdef PK_NO_B
-    for (int q = 0; q < 4; ++q) load_b(here, fb1, q);
-#endif
     issue_a(2, Pos{here.tm, here.tn, 2});
     pk_wait_vmcnt<(SLOTS - 1) * A_LOADS + B_LOADS>();
     __builtin_amdgcn_s_barrier();
@@ -285,13 +407,13 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         here = tile_pos(r);
         const bool has_next = r + 1 < my_tiles;
         const Pos next = has_next ? tile_pos(r + 1) : here;
-        float cb[4];
-        tile_col_bias<GATED>(p, here.tn, wn, fr, cb);
-        float16v acc[4][4];
+        float cb[2];
+        pk_col_bias<GATED>(p, here.tn, wave, fr, cb);
+        float16v acc[8][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = (float16v)0.f;
+            for (int j = 0; j < 2; ++j) acc[i][j] = (float16v)0.f;
         // The tile's first and last stages are peeled: the inner loop's header
         // then only joins states with the same copies in flight, and the
         // compiler's waits for the B registers stay at their steady-state
@@ -309,10 +431,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         here.kt = ktiles - 1;
         stage(g, here, next, has_next, acc, fb1, fb0);
         ++g;
-#ifdef PK_NO_EPI
-        if (p.M == 12345)
-#endif
-        tile_store<GATED>(p, acc, cb, here.tm, here.tn, wm, wn, fr, fk);
+        pk_store<GATED>(p, acc, cb, here.tm, here.tn, wave, fr, fk);
     }
     pk_wait_vmcnt<0>();   // the clamped copies land before the workgroup retires
 }
@@ -323,8 +442,7 @@ bool gemm_packed_ok(const GemmParams& p, bool gated)
     // K % 128: the stage loop runs two stages per trip; K >= 256: the copies
     // run at most one tile ahead
     return p.a_dtype == DT_F16 && p.b_dtype == DT_F16 && p.K % 128 == 0 && p.K >= 256 && p.splits == 1 &&
-           p.batch == 1 &&
-           (size_t)p.M * p.K * 2 < (1u << 31) &&
+           p.batch == 1 && (size_t)p.M * p.K * 2 < (1u << 31) &&
            (size_t)((p.M + 255) / 256) * ((ncols + 255) / 256) >= 128;
 }
 

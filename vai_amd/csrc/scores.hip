@@ -4,15 +4,21 @@
 //
 // The work is bound by writing S (4 bytes per score against ~2 flop/byte of
 // MFMA work per head-dim element), so the kernel is built around the store:
-//  * one workgroup per 128x128 tile of one head; tiles the mask hides
-//    entirely are written as -inf and never touch Q, K or the matrix cores;
+//  * one workgroup per 128x128 tile (64x64 when a mask applies) of one head;
+//    tiles the mask hides entirely are written as -inf and never touch Q, K
+//    or the matrix cores;
 //  * Q and K rows are copied global->LDS (buffer_load ... lds) in 64-wide
-//    head-dim stages, double buffered; 4 waves x (64x64 of 32x32x16 MFMAs);
-//    68 KB of LDS, so two workgroups share a CU and one's stores overlap the
-//    other's loads (measured on MI355X: one workgroup per CU with all of
-//    head_dim in flight is 40% slower, 32-wide stages x 4 is 7% slower);
-//  * the accumulators are staged through LDS and written with scale and mask
-//    applied, 16 bytes per lane, whole 512-byte row segments per wave.
+//    head-dim stages, double buffered; 4 waves x (T/2 x T/2 of 32x32x16
+//    MFMAs); 64 KB (32 KB) of LDS, so two (four) workgroups share a CU and
+//    one's stores overlap the others' loads (measured on MI355X: one
+//    workgroup per CU with all of head_dim in flight is 40% slower, 32-wide
+//    stages x 4 is 7% slower);
+//  * the accumulators are written straight from registers (two 128-byte row
+//    segments per non-temporal store instruction); tiles the mask cuts
+//    through select -inf per output with 32-bit tile-relative compares, and
+//    only tiles at the edges of S test bounds per output.
+#include <algorithm>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -20,14 +26,20 @@
 
 namespace vai_dev {
 
+// cache policy bits of the buffer store builtins: 2 = non-temporal (S is
+// written once and read by the next kernel, not by this one)
+constexpr int kNonTemporal = 2;
+
 namespace sc {
-constexpr int T = 128, BK = 64, CH = BK / 8, RPW = 16 / CH;    // tile, stage depth, chunks per row
-constexpr int SLAB = T * BK * 2;                               // one operand, one stage: 16 KB
-constexpr int STAGE = 2 * SLAB;                                // Q + K
-constexpr int LOADS = STAGE / (4 * 1024);                      // 1 KB copies per wave per stage
-constexpr int EPS = T + 4;                                     // epilogue row stride (floats)
+constexpr int BK = 64, CH = BK / 8, RPW = 16 / CH;             // stage depth, chunks per row
 constexpr int NS = 2;                                          // double buffer
-constexpr int LDS_BYTES = T * EPS * 4 > NS * STAGE ? T * EPS * 4 : NS * STAGE;
+template <int T> struct Tile {
+    static constexpr int WF = T / 64;                          // 32x32 fragments per wave, each way
+    static constexpr int SLAB = T * BK * 2;                    // one operand, one stage
+    static constexpr int STAGE = 2 * SLAB;                     // Q + K
+    static constexpr int LOADS = STAGE / (4 * 1024);           // 1 KB copies per wave per stage
+    static constexpr int LDS_BYTES = NS * STAGE;
+};
 __device__ __forceinline__ int slot(int row, int chunk) { return row * CH + (chunk ^ ((row / RPW) % CH)); }
 }
 
@@ -37,9 +49,11 @@ __device__ __forceinline__ void sc_wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-__global__ __launch_bounds__(256, 2) void scores_kernel(GemmParams p)
+template <int T>
+__global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParams p)
 {
     using namespace sc;
+    constexpr int WF = Tile<T>::WF, STAGE = Tile<T>::STAGE, LOADS = Tile<T>::LOADS, HT = T / 2;
     extern __shared__ half8 lds[];
     LDS_AS char* lds_base = (LDS_AS char*)(LDS_AS void*)lds;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -55,12 +69,17 @@ __global__ __launch_bounds__(256, 2) void scores_kernel(GemmParams p)
         const bool hidden = (p.causal && (int64_t)n0 > last_q) ||
                             (p.span && (int64_t)n0 + T - 1 < first_q + 1 - (int64_t)p.span);
         if (hidden) {
+            // each wave fills its (T/2)x(T/2) block, 16 bytes per lane and
+            // 1 KB per store instruction; rows past M and columns past N are
+            // skipped
+            constexpr int LPR = HT / 4, RPI = 64 / LPR;   // lanes per row, rows per instruction
             const float4v ninf = (float4v)(-__builtin_inff());
-            const bool vec = (N % 4) == 0;
-            for (int i = tid; i < T * (T / 4); i += 256) {
-                const uint32_t r = m0 + i / (T / 4), c = n0 + (i % (T / 4)) * 4;
-                if (r >= M) continue;
-                if (vec && c + 3 < N) *(float4v*)(S + (size_t)r * N + c) = ninf;
+            const uint32_t r0 = m0 + wm * HT, c = n0 + wn * HT + (lane % LPR) * 4;
+            const bool vec = (N % 4) == 0 && c + 3 < N;
+            for (int it = 0; it < HT / RPI; ++it) {
+                const uint32_t r = r0 + it * RPI + lane / LPR;
+                if (r >= M) break;
+                if (vec) __builtin_nontemporal_store(ninf, (float4v*)(S + (size_t)r * N + c));
                 else for (int e = 0; e < 4; ++e) if (c + e < N) S[(size_t)r * N + c + e] = -__builtin_inff();
             }
             return;
@@ -90,17 +109,17 @@ __global__ __launch_bounds__(256, 2) void scores_kernel(GemmParams p)
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             if (isk[i])
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(dst + i * 1024), 16, off[i], kt * BK * 2, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(dst + i * 1024), 16, (int)off[i], kt * BK * 2, 0, 0);
             else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (LDS_AS void*)(dst + i * 1024), 16, off[i], kt * BK * 2, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (LDS_AS void*)(dst + i * 1024), 16, (int)off[i], kt * BK * 2, 0, 0);
         }
     };
 
-    float16v acc[2][2];
+    float16v acc[WF][WF];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WF; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = (float16v)0.f;
+        for (int j = 0; j < WF; ++j) acc[i][j] = (float16v)0.f;
 
     // Up to NS stages in flight from the start; each later stage is issued
     // into the slot the stage before it freed.
@@ -120,15 +139,15 @@ __global__ __launch_bounds__(256, 2) void scores_kernel(GemmParams p)
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int ch = ks * 2 + fk;
-            half8 af[2], bf[2];
+            half8 af[WF], bf[WF];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) af[i] = q[slot(wm * 64 + i * 32 + fr, ch)];
+            for (int i = 0; i < WF; ++i) af[i] = q[slot(wm * HT + i * 32 + fr, ch)];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bf[j] = k[slot(wn * 64 + j * 32 + fr, ch)];
+            for (int j = 0; j < WF; ++j) bf[j] = k[slot(wn * HT + j * 32 + fr, ch)];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < WF; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < WF; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
         if (kt + NS < ktiles) {
@@ -138,38 +157,61 @@ __global__ __launch_bounds__(256, 2) void scores_kernel(GemmParams p)
             issue(kt + NS);
         }
     }
-    __syncthreads();
-
-    // Epilogue through LDS: D[i][j] of a fragment is lane j + 32*((i/4)%2), register (i%4) + 4*(i/8).
-    float* ep = (float*)(lds_base);
-    static_for<2>([&](auto I) __attribute__((always_inline)) {
-        static_for<2>([&](auto J) __attribute__((always_inline)) {
+    // Epilogue straight from the accumulators. D[i][j] of a fragment sits in
+    // lane j + 32*((i/4)%2), register (i%4) + 4*(i/8): per register a
+    // half-wave holds 32 consecutive columns of one row, so each store writes
+    // two 128-byte row segments. Tiles the mask does not touch and that lie
+    // inside S (almost all) store scale * acc through a buffer resource with
+    // no per-output tests; the others apply the mask rule per output.
+    const int64_t q0 = (int64_t)m0 + p.causal_offset;            // query position of the tile's row 0
+    const bool any_mask = (p.causal && (int64_t)n0 + T - 1 > q0) ||
+                          (p.span && (int64_t)n0 < q0 + T - (int64_t)p.span);
+    const float scale = p.scalar_scale;
+    const uint32_t rw0 = wm * HT + 4 * fk, cw0 = wn * HT + fr;     // this lane's row / column in the tile
+    if (m0 + T <= M && n0 + T <= N) {
+        const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(S + (size_t)m0 * N + n0), (short)0, 0x7FFFFFFF, 0x00020000);
+        const uint32_t lane_off = (rw0 * N + cw0) * 4;
+        // mask rule in tile coordinates: with d = n0 - q0 and (rl, cl) the
+        // output's row and column in the tile, causal hides cl - rl > -d;
+        // span hides rl >= span - q0 and cl - rl < 1 - span - d
+        const int d = (int)((int64_t)n0 - q0), lane_diff = (int)cw0 - (int)rw0;
+        const bool causal = p.causal != 0, span = p.span != 0;
+        const int span_row = (int)std::max<int64_t>(std::min<int64_t>((int64_t)p.span - q0, 1 << 30), -(1 << 30));
+        const int span_lim = 1 - (int)p.span - d;
+        static_for<WF>([&](auto I) __attribute__((always_inline)) {
+            static_for<WF>([&](auto J) __attribute__((always_inline)) {
+                static_for<16>([&](auto R) __attribute__((always_inline)) {
+                    constexpr int i = I, j = J, r = R;
+                    constexpr int rc = i * 32 + (r % 4) + 8 * (r / 4);   // row offset of this register
+                    float v = acc[i][j][r] * scale;
+                    if (any_mask) {
+                        const int diff = lane_diff + j * 32 - rc;
+                        const bool hide = (causal && diff > -d) ||
+                                          (span && (int)rw0 + rc >= span_row && diff < span_lim);
+                        v = hide ? -__builtin_inff() : v;
+                    }
+                    const uint32_t voff = lane_off + (uint32_t)rc * N * 4 + j * 128;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out, (int)voff, 0, kNonTemporal);
+                });
+            });
+        });
+        return;
+    }
+    static_for<WF>([&](auto I) __attribute__((always_inline)) {
+        static_for<WF>([&](auto J) __attribute__((always_inline)) {
             static_for<16>([&](auto R) __attribute__((always_inline)) {
                 constexpr int i = I, j = J, r = R;
-                ep[(wm * 64 + i * 32 + 8 * (r / 4) + 4 * fk + (r % 4)) * EPS + wn * 64 + j * 32 + fr] = acc[i][j][r];
+                const uint32_t row = m0 + rw0 + i * 32 + (r % 4) + 8 * (r / 4), col = n0 + cw0 + j * 32;
+                if (row < M && col < N) {
+                    const int64_t pos = (int64_t)row + p.causal_offset, c = col;
+                    const bool hide = (p.causal && c > pos) ||
+                                      (p.span && pos >= (int64_t)p.span && c < pos + 1 - (int64_t)p.span);
+                    S[(size_t)row * N + col] = hide ? -__builtin_inff() : acc[i][j][r] * scale;
+                }
             });
         });
     });
-    __syncthreads();
-    const int c4 = (tid & 31) * 4;
-    const uint32_t col = n0 + c4;
-    const bool vec = (N % 4) == 0 && col + 3 < N;
-    for (int rl = tid >> 5; rl < T; rl += 8) {
-        const uint32_t row = m0 + rl;
-        if (row >= M) break;
-        const float4v v = *(const float4v*)(ep + rl * EPS + c4);
-        const int64_t pos = (int64_t)row + p.causal_offset;
-        float out[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int64_t c = (int64_t)col + e;
-            const bool hide = (p.causal && c > pos) || (p.span && pos >= (int64_t)p.span && c < pos + 1 - (int64_t)p.span);
-            out[e] = hide ? -__builtin_inff() : v[e] * p.scalar_scale;
-        }
-        if (vec) *(float4v*)(S + (size_t)row * N + col) = (float4v){out[0], out[1], out[2], out[3]};
-        else
-            for (int e = 0; e < 4; ++e) if (col + e < N) S[(size_t)row * N + col + e] = out[e];
-    }
 }
 
 bool scores_fast_ok(const GemmParams& p)
@@ -179,18 +221,28 @@ bool scores_fast_ok(const GemmParams& p)
            ((uintptr_t)p.A % 16) == 0 && ((uintptr_t)p.B % 16) == 0;
 }
 
-hipError_t scores_launch(const GemmParams& p, hipStream_t s)
+template <int T>
+static hipError_t scores_launch_t(const GemmParams& p, hipStream_t s)
 {
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)scores_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           sc::LDS_BYTES);
+        hipError_t e = hipFuncSetAttribute((const void*)scores_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           sc::Tile<T>::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    dim3 grid((p.N + sc::T - 1) / sc::T, (p.M + sc::T - 1) / sc::T, p.batch);
-    hipLaunchKernelGGL(scores_kernel, grid, dim3(256), sc::LDS_BYTES, s, p);
+    dim3 grid((p.N + T - 1) / T, (p.M + T - 1) / T, p.batch);
+    hipLaunchKernelGGL(scores_kernel<T>, grid, dim3(256), sc::Tile<T>::LDS_BYTES, s, p);
     return hipGetLastError();
+}
+
+// Masked scores use 64x64 tiles: hidden tiles are then finer, and four
+// times as many workgroups spread the unevenly sized tiles over the CUs
+// (config 4 on MI355X: 12.8 us against 14.1 us with 128x128 tiles); unmasked
+// scores keep 128x128 tiles (fewer Q/K re-reads, 12.8 against 13.2 us).
+hipError_t scores_launch(const GemmParams& p, hipStream_t s)
+{
+    return (p.causal || p.span) ? scores_launch_t<64>(p, s) : scores_launch_t<128>(p, s);
 }
 
 }   // namespace vai_dev

@@ -14,13 +14,19 @@
 //
 // Forward kernel: one workgroup of 8 waves per (32 output channels, one
 // output row, image). It stages the k input rows it needs from NCHW into LDS
-// transposed to [row][column][channel], so 8 channels are one 16-byte LDS
-// read; weight fragments come straight from the packed buffer (L2-resident)
-// into VGPRs. Waves = 4 channel blocks x 2 halves of the 32 output channels;
-// each runs v_mfma_f32_16x16x32_f16 over every tap, their partial sums meet
-// in LDS, and scale, bias, residual and the activation are applied once per
-// output with coalesced stores. Only the input band occupies LDS, so two
+// transposed to [row][column][channel] (8 channels x 8 columns per work item:
+// eight 16-byte loads, a register transpose, eight 16-byte LDS writes), so 8
+// channels are one 16-byte LDS read; weight fragments come straight from the
+// packed buffer (L2-resident) into VGPRs. Waves = 4 channel blocks x 2
+// halves of the 32 output channels; each runs v_mfma_f32_16x16x32_f16 over
+// every tap, their partial sums meet in LDS, and scale, bias, residual and
+// the activation are applied once per output with coalesced stores. A wave
+// stays within 128 VGPRs and only the input band occupies LDS, so two
 // workgroups (16 waves) share a CU and hide each other's latencies.
+// Measured on MI355X (config 5): splitting a row over two workgroups (640
+// of them, three per CU) is 16% slower, and giving each wave every channel
+// block of its own outputs (no LDS sum) is 50% slower -- the weight loads
+// then serialize.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -51,7 +57,7 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(half_t* __restrict__ d
 }
 
 template <int KS, int NF, typename TI>
-__global__ __launch_bounds__(512) void conv_kernel(ConvParams p)
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void conv_kernel(ConvParams p)
 {
     using namespace cv;
     extern __shared__ half8 smem[];
@@ -77,61 +83,51 @@ __global__ __launch_bounds__(512) void conv_kernel(ConvParams p)
     if ((uint32_t)cw < nblk) load_w(cw);
 
     // ---- input rows: NCHW -> LDS [row][pad + w][c] ----
-    // Thread t takes channel c = t % C32 (lanes = consecutive channels, so the
-    // 2-byte LDS writes of a wave land in distinct banks) and every
-    // (512 / C32)-th run of 8 columns.
+    // Work item = 8 channels x 8 columns of one input row: eight 16-byte
+    // (fp16) row loads, a transpose in registers, eight 16-byte LDS writes
+    // (one per column, 8 consecutive channels = one MFMA operand chunk).
+    // Items are ordered channel group fastest: the 16 lanes of a column
+    // group write one contiguous 256-byte channel run (all 64 banks), and a
+    // load instruction reads 64-byte runs of 16 channel rows.
     {
-        const uint32_t nwc = (p.wi + 7) / 8;
-        const uint32_t tpc = 512 / C32 ? 512 / C32 : 1;       // threads per channel
-        const uint32_t c = tid % C32, wc0 = tid / C32;
-        const bool active = (uint32_t)tid < tpc * C32 || C32 > 512;
+        const uint32_t ngc = C32 / 8, ngw = (p.wi + 7) / 8, items = KS * ngc * ngw;
         const size_t plane = (size_t)p.hi * p.wi;
         const bool vec = p.wi % 8 == 0 && ((uintptr_t)p.x % (8 * sizeof(TI))) == 0;
-        for (uint32_t cc = c; cc < C32; cc += 512) {
+        for (uint32_t it = tid; it < items; it += 512) {
+            const uint32_t cg = it % ngc, rest = it / ngc, wg = rest % ngw, r = rest / ngw;
+            const int hi = (int)(ho * p.stride) + (int)r - PAD;
+            const bool row_ok = hi >= 0 && hi < (int)p.hi;
+            const uint32_t c0 = cg * 8, w0 = wg * 8;
+            half8 col[8];
 #pragma unroll
-            for (int r = 0; r < KS; ++r) {
-                const int hi = (int)(ho * p.stride) + r - PAD;
-                const bool row_ok = hi >= 0 && hi < (int)p.hi && cc < p.ci;
-                half_t* dst = xs + ((size_t)r * WiP) * CIP + cc;
-                if (wc0 == 0 && active) {
+            for (int j = 0; j < 8; ++j) col[j] = (half8)(half_t)0;
+            if (row_ok) {
 #pragma unroll
-                    for (int e = 0; e < PAD; ++e) {
-                        dst[(size_t)e * CIP] = (half_t)0;
-                        dst[(size_t)(PAD + p.wi + e) * CIP] = (half_t)0;
-                    }
-                }
-                if (!active) continue;
-                const TI* src = (const TI*)p.x + ((size_t)b * p.ci + (cc < p.ci ? cc : 0)) * plane +
-                                (size_t)(row_ok ? hi : 0) * p.wi;
-                for (uint32_t wb = wc0; wb < nwc; wb += 4 * tpc) {
-                    float v[4][8];
-                    if (vec) {   // wi % 8 == 0: one 16- (fp16) or 32-byte (fp32) load per run
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const uint32_t w0 = (wb + u * tpc) * 8;
-                            typedef TI tv8 __attribute__((ext_vector_type(8)));
-                            const tv8 t = (row_ok && w0 < p.wi) ? *(const tv8*)(src + w0) : (tv8)0;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) v[u][e] = (float)t[e];
-                        }
+                for (int e = 0; e < 8; ++e) {
+                    if (c0 + e >= p.ci) continue;
+                    const TI* src = (const TI*)p.x + ((size_t)b * p.ci + c0 + e) * plane + (size_t)hi * p.wi + w0;
+                    typedef TI tv8 __attribute__((ext_vector_type(8)));
+                    tv8 t;
+                    if (vec) {
+                        t = *(const tv8*)src;
                     } else {
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const uint32_t w0 = (wb + u * tpc) * 8;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e)
-                                v[u][e] = (row_ok && w0 + e < p.wi) ? (float)src[w0 + e] : 0.f;
-                        }
+                        for (int j = 0; j < 8; ++j) t[j] = w0 + j < p.wi ? src[j] : (TI)0;
                     }
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const uint32_t w0 = (wb + u * tpc) * 8;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            if (w0 + e < p.wi) dst[(size_t)(PAD + w0 + e) * CIP] = (half_t)v[u][e];
-                    }
+                    for (int j = 0; j < 8; ++j) col[j][e] = (half_t)t[j];
                 }
             }
+            half_t* dst = xs + ((size_t)r * WiP + PAD + w0) * CIP + c0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (w0 + j < p.wi) *(half8*)(dst + (size_t)j * CIP) = col[j];
+        }
+        // the zero padding columns
+        for (uint32_t i = tid; i < (uint32_t)(KS * 2 * PAD) * (C32 / 8); i += 512) {
+            const uint32_t cg = i % (C32 / 8), rc = i / (C32 / 8), r = rc / (2 * PAD), e = rc % (2 * PAD);
+            const uint32_t w = e < PAD ? e : PAD + p.wi + (e - PAD);
+            *(half8*)(xs + ((size_t)r * WiP + w) * CIP + cg * 8) = (half8)(half_t)0;
         }
     }
     __syncthreads();

@@ -170,3 +170,52 @@ def test_gpt2_cfc_through_the_engine(gpu):
     got = forward(net, {"in0": x})
     assert net.node.plan.startswith("tile_f32")
     assert_close(got[C.CFG1_ROWS], G["cfg1_rows"], FP32)
+
+
+def test_linear_node_packs_prefill_weight(gpu):
+    """A prefill-sized fp16 Linear packs its weight once at prepare and runs
+    the packed-weight GEMM; decode-sized inputs on the same net take the
+    GEMV; a new weight tensor is packed again."""
+    pv = pyvai()
+    rng = np.random.default_rng(0)
+    m, k, n = 1024, 512, 8192
+    w = draw(normal((n, k), 0.05), rng, np.float16)
+    b = draw(normal((n,), 0.05), rng, np.float16)
+    x = draw((m, k), rng, np.float16)
+    net = build_net(lambda: pv.nodes.LinearNode(in_dim=k, out_dim=n, epilogue=pv.Epilogue.GELU_TANH),
+                    ["in0"], {"weight": w, "bias": b}, w_dtype="F16")
+    got = forward(net, {"in0": x})
+    assert net.node.plan == "tile_f16_256x256_packed", net.node.plan
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(m - 4, m), rng.choice(m, 16, replace=False)]))
+    assert_close(got[rows], oracle.linear(x[rows], w, b, epi="GELU_TANH", stage="tile"), TRANS)
+    # decode shape on the same net: the slab GEMV on the unpacked weight
+    xs = draw((2, k), rng, np.float16)
+    got_s = forward(net, {"in0": xs})
+    assert net.node.plan.startswith("slab"), net.node.plan
+    assert_close(got_s, oracle.linear(xs, w, b, epi="GELU_TANH"), TRANS)
+    # a new weight is packed again
+    w2 = draw(normal((n, k), 0.05), rng, np.float16)
+    net.node["weight"] = pv.Tensor.from_numpy(w2)
+    got2 = forward(net, {"in0": x})
+    assert net.node.plan == "tile_f16_256x256_packed"
+    assert_close(got2[rows], oracle.linear(x[rows], w2, b, epi="GELU_TANH", stage="tile"), TRANS)
+
+
+def test_gated_ffn_packed_fusion(gpu):
+    """The fused gate/up GEMM at prefill size runs on the packed weight (the
+    gated layout), equal to the unfused two-kernel path bit for bit."""
+    pv = pyvai()
+    rng = np.random.default_rng(0)
+    m, k, h = 2048, 512, 4096
+    w = draw(normal((2 * h, k), 0.05), rng, np.float16)
+    x = draw((m, k), rng, np.float16)
+    outs = {}
+    for fuse in (True, False):
+        net = _ffn_net(pv, k, h, fuse)
+        net.gate_up["weight"] = pv.Tensor.from_numpy(w)
+        outs[fuse] = forward(net, {"in0": x})
+        assert net.gate_up.plan == ("tile_f16_256x256_packed_gated" if fuse else "tile_f16_256x256_packed")
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(m - 4, m), rng.choice(m, 16, replace=False)]))
+    want = oracle.gated_mul(oracle.linear(x[rows], w, stage="tile"), epi="SILU")
+    assert_close(outs[True][rows], want, TRANS)
+    assert_close(outs[False][rows], want, TRANS)

@@ -273,6 +273,14 @@ void NeuralNet::operator()(TensorDict inputs, TensorRefDict outputs, bool syncPr
         needToRebuildGraph_ = false;
         needToUploadParams_ = true;
     }
+    // A parameter set after the first forward (a new weight tensor on a
+    // node) still has only host data: upload it and record again.
+    if (!needToUploadParams_)
+        for (Node* n : sortedNodes_)
+            for (auto& [name, sl] : n->slots_)
+                if (sl.type_ == NodeSlot::persistent && sl.value_.validShape() && sl.value_.hasHostData() &&
+                    !sl.value_.gpuBufferBound())
+                    needToUploadParams_ = true;
     if (needToUploadParams_) {
         uploadModelParams();
         needToUploadParams_ = false;

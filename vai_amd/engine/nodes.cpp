@@ -80,7 +80,7 @@ vai_linear_args Linear::args(bool withPointers) const
 
 bool Linear::packedMatches(const vai_linear_args& a) const
 {
-    return packed_ && packedFrom_ == (*this)["weight"].devicePtr() && packedGated_ == (a.gated != 0);
+    return packed_ && packedFrom_ == (*this)["weight"].uploadId() && packedGated_ == (a.gated != 0);
 }
 
 bool Linear::canFuseGate(const GatedMul& gm) const
@@ -123,13 +123,13 @@ void Linear::prepare()
     // the matrix cores; it is made once per weight buffer and layout (a fused
     // gate changes the layout), as the reference prepares its weights once.
     const size_t pbytes = M_ > 8 ? vai_linear_packed_weight_size(&a) : 0;
-    if (pbytes && (packedFrom_ != w.devicePtr() || packedGated_ != (a.gated != 0))) {
+    if (pbytes && (!packed_ || packedFrom_ != w.uploadId() || packedGated_ != (a.gated != 0))) {
         packed_ = bufferPool().requestBuffer(pbytes);
         vai_linear_args pa = a;
         pa.weight = w.devicePtr();
         check(vai_linear_pack_weight(&pa, packed_.ptr(), packed_.size(), (vai_stream_t)net().stream()), "Linear");
         check(vai_stream_sync((vai_stream_t)net().stream()), "Linear");
-        packedFrom_ = w.devicePtr();
+        packedFrom_ = w.uploadId();
         packedGated_ = a.gated != 0;
     }
     a.packed_weight = packedMatches(a) ? packed_.ptr() : nullptr;
@@ -265,15 +265,15 @@ void Convolution::prepare()
         require(r.isShapeOf(os) && r.dtype() == in.dtype(), "Convolution: residual must match the output, input dtype");
     }
     // The weight is packed once, like the reference's one-shot transform
-    // (convolution.h:6224-6235); a new weight buffer repacks.
+    // (convolution.h:6224-6235); a new weight upload repacks.
     vai_conv2d_args a = args(false);
     const size_t pbytes = vai_conv2d_packed_weight_size(&a);
-    if (pbytes && packedFrom_ != w.devicePtr()) {
+    if (pbytes && (!packed_ || packedFrom_ != w.uploadId())) {
         packed_ = bufferPool().requestBuffer(pbytes);
         a.weight = w.devicePtr();
         check(vai_conv2d_pack_weight(&a, packed_.ptr(), packed_.size(), (vai_stream_t)net().stream()), "Convolution");
         check(vai_stream_sync((vai_stream_t)net().stream()), "Convolution");
-        packedFrom_ = w.devicePtr();
+        packedFrom_ = w.uploadId();
     }
     (*this)["split"] = Tensor();
 }

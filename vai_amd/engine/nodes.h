@@ -69,7 +69,7 @@ private:
     Dtype accDtype_ = Dtype::None;
     GatedMul* fused_ = nullptr;
     PooledBuffer packed_;              // fragment-major copy of the weight for prefill shapes
-    const void* packedFrom_ = nullptr;
+    uint64_t packedFrom_ = 0;          // uploadId() of the weight it was made from
     bool packedGated_ = false;
     uint32_t M_ = 0, biasRepeat_ = 0, residualRepeat_ = 0;
     std::string plan_;
@@ -121,7 +121,7 @@ public:
 private:
     vai_conv2d_args args(bool withPointers) const;
     PooledBuffer packed_;          // weight packed once for the fp16 kernel
-    const void* packedFrom_ = nullptr;
+    uint64_t packedFrom_ = 0;      // uploadId() of the weight it was made from
     uint32_t batch_ = 1, hi_ = 0, wi_ = 0;
 };
 

@@ -1,6 +1,8 @@
 // tensor.cpp -- host conversions, layout helpers and host<->device copies of vai::Tensor.
 #include "tensor.h"
 
+#include <atomic>
+
 #include <algorithm>
 #include <bit>
 #include <numeric>
@@ -199,6 +201,8 @@ void Tensor::upload(void* stream)
     const vai_status st = vai_memcpy_h2d(devicePtr(), data_->hostData_.data(), numBytes(), (vai_stream_t)stream);
     require(st == VAI_OK, std::string("upload: ") + vai_status_string(st));
     data_->hostUploaded_ = true;
+    static std::atomic<uint64_t> uploads{0};
+    data_->uploadId_ = ++uploads;
 }
 
 Tensor& Tensor::downloadToHost()

@@ -46,6 +46,7 @@ class TensorData
 
     HostBuffer hostData_;
     bool hostUploaded_ = false;     // hostData_ is already on the device; a setter clears it
+    uint64_t uploadId_ = 0;         // distinct per upload: identifies the device contents
     const Dtype dtype_;
     PooledBuffer buffer_;
     std::pair<NeuralNet*, uint64_t> lastSubmission_{nullptr, 0};
@@ -122,6 +123,9 @@ public:
     bool hasHostData() const { return data_ && !data_->hostData_.empty(); }
     const void* hostData() const { return hasHostData() ? data_->hostData_.data() : nullptr; }
     bool gpuBufferBound() const { return data_ && data_->buffer_; }
+    // Changes on every upload of host data (device pointers can repeat when
+    // the pool hands a released buffer out again).
+    uint64_t uploadId() const { return data_ ? data_->uploadId_ : 0; }
     uint32_t baseOffset() const { return baseOffset_; }
     // Device address of element 0 of this tensor (the Vulkan BufferRange's role).
     void* devicePtr() const;

@@ -68,7 +68,8 @@ class Case:
 
 def load_traffic():
     """HBM bytes per launch from the committed rocprofv3 counter table:
-    workload key -> FETCH_FACTOR * FETCH_SIZE + WRITE_FACTOR * WRITE_SIZE."""
+    workload key -> FETCH_FACTOR * FETCH_SIZE + WRITE_FACTOR * WRITE_SIZE, summed
+    over the rows of one key (a split-K GEMM and its reduce are one step)."""
     out = {}
     if not os.path.exists(TRAFFIC_FILE):
         return out
@@ -76,7 +77,7 @@ def load_traffic():
         if ln.startswith("#") or not ln.strip():
             continue
         key, _kernel, fetch_kib, write_kib = ln.rstrip("\n").split("\t")
-        out[key] = round((FETCH_FACTOR * float(fetch_kib) + WRITE_FACTOR * float(write_kib)) * 1024)
+        out[key] = out.get(key, 0) + round((FETCH_FACTOR * float(fetch_kib) + WRITE_FACTOR * float(write_kib)) * 1024)
     return out
 
 

@@ -37,3 +37,15 @@ def test_gated_ffn_net_from_cpp(gpu, tmp_path, m, k, h, plan):
     got = np.fromfile(tmp_path / "y.f32", np.float32).reshape(m, h)
     want = oracle.gated_mul(oracle.linear(x, w, b), epi="SILU")
     assert_close(got, want, TRANS)
+
+
+@pytest.mark.gpu
+def test_mfma_rate_program(gpu):
+    """tests/cpp/mfma_rate measures the fp16 MFMA ceiling with constant and
+    with random operands (the roofline figures in the bench notes come from
+    it); here it runs briefly and must report six positive rates."""
+    exe = os.path.join(os.path.dirname(BIN), "mfma_rate")
+    r = subprocess.run([exe, "200"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    rates = [float(l.split(",")[1].split()[0]) for l in r.stdout.splitlines() if "TFLOP/s" in l]
+    assert len(rates) == 6 and all(v > 0 for v in rates), r.stdout

@@ -237,7 +237,21 @@ def test_linear_packed_weight(gpu, m, k, n, gated, odt, epi, residual, bias):
     assert_close(got[rows].astype(np.float32), want.astype(np.float32), tol)
     # same MFMA order as the LDS-staged kernel: bit-identical outputs
     ref = run_linear(gpu, x, w, b, r, out_dtype=odt, **kw)
-    np.testing.assert_array_equal(got, ref)
+    diff = got != ref
+    if diff.any():
+        # say where, and which of the two kernels the oracle sides with
+        rr, cc = np.nonzero(diff)
+        rows_bad = np.unique(rr)[:8]
+        if gated:
+            w_rows = oracle.gated_mul(oracle.linear(x[rows_bad], w, b, stage="tile"), epi=epi, out_dtype=odt)
+        else:
+            w_rows = oracle.linear(x[rows_bad], w, b, r, epi=epi, out_dtype=odt, stage="tile")
+        e_packed = np.abs(got[rows_bad].astype(np.float64) - w_rows).max()
+        e_lds = np.abs(ref[rows_bad].astype(np.float64) - w_rows).max()
+        pytest.fail(f"{diff.sum()} outputs differ; rows {np.unique(rr)[:16]} (of {len(np.unique(rr))}), "
+                    f"cols {np.unique(cc)[:16]} (of {len(np.unique(cc))}); rows % 256 {np.unique(rr % 256)[:16]}, "
+                    f"cols % 128 {np.unique(cc % 128)[:16]}; max error vs oracle on those rows: packed {e_packed:.3g}, "
+                    f"LDS-staged {e_lds:.3g}")
 
 
 def test_linear_packed_weight_rejects(gpu):

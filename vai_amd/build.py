@@ -46,7 +46,7 @@ def _build_pymodule():
     out = os.path.join(HERE, "_pyvai" + ext)
     obj = os.path.join(BUILD, "pyvai.o")
     inc = ["-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"]]
-    cmd = [HIPCC, "-x", "hip", "-O2", "-fPIC", "-std=c++20", f"--offload-arch={ARCH}", "-I",
+    cmd = [HIPCC, "-x", "hip", "-O2", "-fPIC", "-std=c++20", f"--offload-arch={ARCH}"] + DEVICE_FLAGS + ["-I",
            os.path.join(ROOT, "include"), "-I", HERE] + inc + ["-c", PYMOD_SRC, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -98,7 +98,7 @@ def _build_cpp_programs():
         if not f.endswith(".cpp"):
             continue
         out = os.path.join(CPP_TEST_BIN, f[:-4])
-        cmd = [HIPCC, "-x", "hip", "-O2", "-std=c++20", f"--offload-arch={ARCH}", "-I", os.path.join(ROOT, "include"),
+        cmd = [HIPCC, "-x", "hip", "-O2", "-std=c++20", f"--offload-arch={ARCH}"] + DEVICE_FLAGS + ["-I", os.path.join(ROOT, "include"),
                "-I", ENGINE, os.path.join(CPP_TESTS, f), "-o", out + ".tmp", "-L", HERE, "-lvai_amd",
                "-Wl,-rpath," + os.path.relpath(HERE, CPP_TEST_BIN).join(["$ORIGIN/", ""])]
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -48,4 +48,4 @@ def test_mfma_rate_program(gpu):
     r = subprocess.run([exe, "200"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     rates = [float(l.split(",")[1].split()[0]) for l in r.stdout.splitlines() if "TFLOP/s" in l]
-    assert len(rates) == 6 and all(v > 0 for v in rates), r.stdout
+    assert len(rates) == 12 and all(v > 0 for v in rates), r.stdout

@@ -266,3 +266,34 @@ def test_linear_packed_weight_rejects(gpu):
     assert n == 2 * 8 * 384 * 64
     small = D((n - 16,), np.uint8)
     assert gpu.lib().vai_linear_pack_weight(ctypes.byref(a), small.ptr, small.nbytes, None) == 1004
+
+
+@pytest.mark.parametrize("m, k, n, bias, res, order, odt, epi", [
+    (128, 768, 3072, "row", None, 0, np.float32, "GELU_TANH"),   # config 1's shape, 32x48 tiles
+    (9, 32, 16, "row", None, 0, np.float32, "NONE"),              # one K stage: waves 1-3 idle
+    (33, 96, 100, "full", "full", 1, np.float32, "RELU"),         # ragged M and N, 3 stages
+    (100, 800, 130, None, "row", 0, np.float16, "SILU"),          # fp16 output, [N] residual
+    (64, 1024, 1000, "row", "full", 0, np.float32, "SIGMOID"),
+    (200, 288, 60, "row", None, 0, np.float32, "GELU"),           # 9 stages: not a multiple of 4
+    (40, 7 * 32 * 4, 50, "row", None, 0, np.float32, "NONE"),     # 7 stages per wave: ring tail of 1
+])
+def test_linear_f32_small(gpu, m, k, n, bias, res, order, odt, epi):
+    """The one-launch fp32 path (32 x 16*nf tiles, K split over the four
+    waves and summed in LDS) vs the oracle and the float64 closed form."""
+    rng = np.random.default_rng(3)
+    w = draw(normal((n, k), 1.0 / np.sqrt(k)), rng)
+    b = draw((n,) if bias == "row" else (m, n), rng) if bias else None
+    x = draw((m, k), rng)
+    r = draw((n,) if res == "row" else (m, n), rng, odt) if res else None
+    D = gpu.DeviceArray.from_numpy
+    a = gpu.linear_args(gpu.DeviceArray((m, n), odt), D(x), D(w), D(b) if bias else None, D(r) if res else None,
+                        epi=epi, order=order)
+    name, splits = gpu.linear_plan(a)
+    assert name.startswith("tile_f32_32x") and splits == 1, name
+    assert gpu.lib().vai_linear_workspace_size(ctypes.byref(a)) == 0
+    got = run_linear(gpu, x, w, b, r, out_dtype=odt, epi=epi, order=order)
+    want = oracle.linear(x, w, b, r, epi=epi, order=order, out_dtype=odt)
+    tol = FP16 if odt == np.float16 else (FP32 if epi in ("NONE", "RELU") else TRANS)
+    assert_close(got.astype(np.float32), want.astype(np.float32), tol)
+    again = run_linear(gpu, x, w, b, r, out_dtype=odt, epi=epi, order=order)
+    np.testing.assert_array_equal(again, got)

@@ -26,7 +26,7 @@ size_t dtype_bytes(int32_t d) { return d == VAI_DTYPE_F16 ? 2 : 4; }
 vai_status hip_status(hipError_t e) { return e == hipSuccess ? VAI_OK : (vai_status)e; }
 
 struct LinearPlan {
-    enum Kind { Slab, SlabThenGate, Tile, BigTile, PackedTile } kind;
+    enum Kind { Slab, SlabThenGate, Tile, BigTile, PackedTile, F32Small } kind;
     GemmTile tile;
     uint32_t bm, bn;
     uint32_t split_size, splits;
@@ -76,6 +76,18 @@ LinearPlan plan_linear(const vai_linear_args* a)
         g.A = a->in; g.B = a->weight; g.splits = 1; g.batch = 1;
         if (a->split_size == 0 && a->packed_weight && gemm_packed_ok(g, a->gated)) {
             p.kind = LinearPlan::PackedTile;
+            p.splits = 1;
+            p.split_size = K;
+            p.workspace = 0;
+            return p;
+        }
+        // fp32 problems with fewer 64x64 tiles than CUs: one launch over the
+        // full K with a CU-filling tile count, instead of split-K + reduce
+        if (a->split_size == 0 && !a->gated && gemm_f32_ok(g) && tiles_of(M, N, 64, 64) < kCUs) {
+            const int nf = gemm_f32_nf(M, N, kCUs);
+            p.kind = LinearPlan::F32Small;
+            p.bm = 32;
+            p.bn = 16 * nf;
             p.splits = 1;
             p.split_size = K;
             p.workspace = 0;
@@ -163,6 +175,8 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
         sp.M = a->M;
         snprintf(buf, sizeof buf, "%s%s", (sp.M >= 2 && gemv_mfma_ok(sp)) ? "slab_mfma" : slab_vec_ok(sp) ? "slab" : "slab_scalar",
                  p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
+    } else if (p.kind == LinearPlan::F32Small) {
+        snprintf(buf, sizeof buf, "tile_f32_32x%u_kwaves", p.bn);
     } else if (p.kind == LinearPlan::BigTile || p.kind == LinearPlan::PackedTile) {
         snprintf(buf, sizeof buf, "tile_f16_256x256%s%s", p.kind == LinearPlan::PackedTile ? "_packed" : "",
                  a->gated ? "_gated" : "");
@@ -219,6 +233,7 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
     else { g.C = a->out; g.c_dtype = a->o_dtype; }
     if (p.kind == LinearPlan::PackedTile) return hip_status(gemm_packed_launch(g, a->packed_weight, a->gated != 0, s));
     if (p.kind == LinearPlan::BigTile) return hip_status(gemm_big_launch(g, a->gated != 0, s));
+    if (p.kind == LinearPlan::F32Small) return hip_status(gemm_f32_launch(g, (int)(p.bn / 16), s));
     hipError_t e = gemm_launch(g, a->gated ? BKind::Gated : BKind::Dense,
                                a->gated ? EpiKind::Gated : EpiKind::Linear, p.tile, s);
     if (e != hipSuccess || p.splits == 1) return hip_status(e);

@@ -86,6 +86,12 @@ size_t gemm_packed_weight_bytes(uint32_t N, uint32_t K, uint32_t H, bool gated);
 hipError_t gemm_pack_weight(void* dst, const void* w, uint32_t N, uint32_t K, uint32_t H, bool gated, hipStream_t s);
 hipError_t gemm_packed_launch(const GemmParams& p, const void* packed, bool gated, hipStream_t s);
 
+// fp32 Linear for small problems: a 32 x 16*nf tile per workgroup over the
+// full K (the waves split K and sum through LDS), no split-K workspace.
+bool gemm_f32_ok(const GemmParams& p);
+int gemm_f32_nf(uint32_t M, uint32_t N, uint32_t cus);
+hipError_t gemm_f32_launch(const GemmParams& p, int nf, hipStream_t s);
+
 // Attention scores for fp16 Q/K with head_dim % 64 == 0.
 bool scores_fast_ok(const GemmParams& p);
 hipError_t scores_launch(const GemmParams& p, hipStream_t s);

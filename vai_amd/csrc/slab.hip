@@ -15,6 +15,10 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <algorithm>
+
+#define LDS_AS __attribute__((address_space(3)))
+
 namespace vai_dev {
 
 template <typename T> struct Vec16;
@@ -217,40 +221,53 @@ __global__ __launch_bounds__(256) void slab_scalar_kernel(SlabParams a)
     }
 }
 
-// fp16 I and W, M <= 16: the GEMV on v_mfma_f32_16x16x32_f16. A = I padded
-// to 16 rows (rows >= M read as zero), B = 16 rows of W. fp16 products are
-// exact in fp32 and accumulate in fp32, the slab contract, while the matrix
-// core keeps the arithmetic off the VALU: at M = 8 the FMA path costs more
-// than the 32 MB HBM stream it overlaps. A workgroup owns 16 W rows; its 4
-// waves take a quarter of K each, issue all their 16-byte non-temporal W
-// loads up front, and sum their 16x16 partials through LDS.
-__global__ __launch_bounds__(256) void gemv_mfma_kernel(SlabParams a)
+// fp16 I and W, 2 <= M <= 16: the GEMV on v_mfma_f32_16x16x32_f16. A = I
+// padded to 16 rows (rows >= M read as zero), B = 16 rows of W. fp16 products
+// are exact in fp32 and accumulate in fp32, the slab contract, while the
+// matrix core keeps the arithmetic off the VALU (at M = 8 the FMA path costs
+// more than the 32 MB HBM stream it overlaps). A workgroup owns 16 W rows;
+// wave w takes the K quarter [w*K/4, (w+1)*K/4) through a private 16 KB LDS
+// region, 512 k per pass, and the four 16x16 partials meet in LDS at the end.
+// W goes global -> LDS by buffer_load ... lds, 1 KB of one row per copy
+// instruction, and the fragments are read back from LDS; the 16-byte chunks
+// of row r sit at chunk ^ r, so a fragment read (16 rows, one chunk) hits
+// distinct banks. (Loading fragments straight from W, 16 rows x 64 bytes per
+// load instruction, measured 2-3% slower.)
+__global__ __launch_bounds__(256) void gemv_lds_kernel(SlabParams a)
 {
-    constexpr int BATCH = 16;                     // 16-byte W loads per lane in flight
+    extern __shared__ half8 gl_lds[];
     __shared__ float part[4][16][17];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n0 = blockIdx.x * 16, K = a.K, N = a.N, M = a.M;
     const int fr = lane & 15, fg = lane >> 4;
     const uint32_t kq = K / 4, kbeg = wave * kq;
-    const half_t* __restrict__ W = (const half_t*)a.weight;
-    const half_t* __restrict__ X = (const half_t*)a.in;
-    const uint32_t wrow = min(n0 + fr, N - 1);
-    const half_t* wp = W + (size_t)wrow * K + kbeg + fg * 8;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const half_t*)a.weight + (size_t)n0 * K), (short)0,
+        (int)std::min<size_t>((size_t)(N - n0) * K * 2, 0x7FFFFFFF), 0x00020000);
+    LDS_AS char* region = (LDS_AS char*)(LDS_AS void*)gl_lds + wave * 16384;
     const bool xrow_ok = (uint32_t)fr < M;
-    const half_t* xp = X + (size_t)(xrow_ok ? fr : 0) * K + kbeg + fg * 8;
+    const half_t* xp = (const half_t*)a.in + (size_t)(xrow_ok ? fr : 0) * K + kbeg + fg * 8;
     float4v acc = (float4v)0.f;
-    for (uint32_t k = 0; k < kq; k += 32 * BATCH) {
-        half8 wv[BATCH], xv[BATCH];
+    for (uint32_t k = 0; k < kq; k += 512) {
+        // row r: lane l copies logical chunk l ^ r of the row's 1 KB
 #pragma unroll
-        for (int i = 0; i < BATCH; ++i)
-            wv[i] = (k + i * 32 < kq) ? __builtin_nontemporal_load((const half8*)(wp + k + i * 32)) : (half8)0;
+        for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (LDS_AS void*)(region + r * 1024), 16,
+                                                     (int)((r * K + kbeg + k) * 2 + (lane ^ r) * 16), 0, 0, 0);
+        half8 xv[16];
 #pragma unroll
-        for (int i = 0; i < BATCH; ++i)
+        for (int i = 0; i < 16; ++i)
             xv[i] = (xrow_ok && k + i * 32 < kq) ? *(const half8*)(xp + k + i * 32) : (half8)0;
+        __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));   // vmcnt(0)
 #pragma unroll
-        for (int i = 0; i < BATCH; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[i], wv[i], acc, 0, 0, 0);
+        for (int i = 0; i < 16; ++i) {
+            const int c = 4 * i + fg;   // logical chunk of k = k + 32 i + 8 fg
+            half8 wv = *(LDS_AS const half8*)(region + fr * 1024 + ((c ^ fr) * 16));
+            if (k + i * 32 >= kq) wv = (half8)0;
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[i], wv, acc, 0, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): region free
     }
-    // D[i][j] (i = input row m, j = W row) sits in lane j + 16*(i/4), register i%4.
 #pragma unroll
     for (int r = 0; r < 4; ++r) part[wave][fg * 4 + r][fr] = acc[r];
     __syncthreads();
@@ -301,7 +318,14 @@ bool slab_vec_ok(const SlabParams& a)
 hipError_t slab_launch(const SlabParams& a, hipStream_t s)
 {
     if (a.M >= 2 && gemv_mfma_ok(a)) {
-        hipLaunchKernelGGL(gemv_mfma_kernel, dim3((a.N + 15) / 16), dim3(256), 0, s, a);
+        static bool attr_set = false;   // 64 KB dynamic + the static partial-sum array
+        if (!attr_set) {
+            hipError_t e = hipFuncSetAttribute((const void*)gemv_lds_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(gemv_lds_kernel, dim3((a.N + 15) / 16), dim3(256), 65536, s, a);
         return hipGetLastError();
     }
     if (slab_vec_ok(a)) {

@@ -123,8 +123,9 @@ vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int3
  * weights (Convolution::validateInputs, /root/reference/vai/nodes/
  * convolution.h:4137-4160). Replaces runK3S1Implicit / the implicit-GEMM
  * plan (/root/reference/vai/nodes/convolution.h:6237-6283, 6616-6644).
- * With fp16 weights the kernel reads them packed [tap][co][ci] (channels
- * padded to a multiple of 32): pass a buffer that vai_conv2d_pack_weight()
+ * With fp16 weights the kernel reads them packed per tap in MFMA fragment
+ * order (output channels padded to a multiple of 16, input channels to a
+ * multiple of 32): pass a buffer that vai_conv2d_pack_weight()
  * filled once as packed_weight (the reference transforms conv weights once,
  * /root/reference/vai/nodes/convolution.h:6224-6235), or leave it NULL and
  * pass a workspace of vai_conv2d_workspace_size() bytes in which every call

@@ -8,16 +8,18 @@
 // The reduction index is (tap, channel) here instead of the reference's
 // c*k*k + tap: the order of an fp32 sum is free, and this one makes 8
 // consecutive k values 8 consecutive channels, which is what one MFMA lane
-// consumes. Weights are packed once to that order, [tap][co][c] with channels
-// zero-padded to a multiple of 32 (the reference transforms conv weights once
-// too, convolution.h:6224-6235).
+// consumes. Weights are packed once to that order, in MFMA fragment order
+// with channels zero-padded to a multiple of 32 (the reference transforms
+// conv weights once too, convolution.h:6224-6235).
 //
 // Forward kernel: one workgroup of 8 waves per (32 output channels, one
 // output row, image). It stages the k input rows it needs from NCHW into LDS
 // transposed to [row][column][channel] (8 channels x 8 columns per work item:
 // eight 16-byte loads, a register transpose, eight 16-byte LDS writes), so 8
 // channels are one 16-byte LDS read; weight fragments come straight from the
-// packed buffer (L2-resident) into VGPRs. Waves = 4 channel blocks x 2
+// packed buffer (L2-resident) into VGPRs, 1 KB of contiguous memory per
+// tap and wave (packing [tap][co][c] instead, a fragment load reads 16 rows x
+// 64 bytes and the loads cost 25% of the kernel time). Waves = 4 channel blocks x 2
 // halves of the 32 output channels; each runs v_mfma_f32_16x16x32_f16 over
 // every tap, their partial sums meet in LDS, and scale, bias, residual and
 // the activation are applied once per output with coalesced stores. A wave
@@ -39,20 +41,33 @@ inline __host__ __device__ uint32_t ci32(uint32_t ci) { return (ci + 31) / 32 * 
 inline __host__ __device__ uint32_t cip(uint32_t ci) { return ci32(ci) + 8; }   // LDS row stride (halves)
 }
 
-// W [Co, C, k, k] (fp16) -> Wp [k*k][Co][C32] fp16, zero-padded channels.
-// One workgroup per output channel: its C*k*k weights are read contiguously
-// into LDS and written out tap-major.
+// W [Co, C, k, k] (fp16) -> the fragment-major packed weight: for tap t,
+// 16-channel output block o, 32-channel input block cb and MFMA lane l
+// (output channel o*16 + l%16, input channels cb*32 + 8*(l/16) .. +7):
+//   Wp[((t*CO16 + o)*NB + cb)*64 + l][0..7],  CO16 = ceil(Co/16), NB = C32/32
+// so a wave's A fragment of one tap is 1 KB of contiguous memory. Padding
+// output channels and input channels past C are zero. One workgroup per
+// (padded) output channel: its C*k*k weights are read contiguously into LDS
+// and written out in 16-byte chunks.
 __global__ __launch_bounds__(256) void pack_weight_kernel(half_t* __restrict__ dst, const half_t* __restrict__ w,
                                                           uint32_t Co, uint32_t C, uint32_t C32, uint32_t kk)
 {
     extern __shared__ half_t row[];
-    const uint32_t co = blockIdx.x;
+    const uint32_t co = blockIdx.x, CO16 = gridDim.x / 16, NB = C32 / 32;
     const size_t n = (size_t)C * kk;
-    for (size_t i = threadIdx.x; i < n; i += 256) row[i] = w[(size_t)co * n + i];
+    if (co < Co)
+        for (size_t i = threadIdx.x; i < n; i += 256) row[i] = w[(size_t)co * n + i];
     __syncthreads();
-    for (size_t i = threadIdx.x; i < (size_t)kk * C32; i += 256) {
-        const uint32_t c = i % C32, tap = i / C32;
-        dst[((size_t)tap * Co + co) * C32 + c] = c < C ? row[(size_t)c * kk + tap] : (half_t)0;
+    for (uint32_t i = threadIdx.x; i < kk * (C32 / 8); i += 256) {
+        const uint32_t chunk = i % (C32 / 8), tap = i / (C32 / 8), cb = chunk / 4, fg = chunk % 4;
+        half8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t c = chunk * 8 + e;
+            v[e] = (co < Co && c < C) ? row[(size_t)c * kk + tap] : (half_t)0;
+        }
+        const size_t lane = co % 16 + 16 * fg;
+        *(half8*)(dst + ((((size_t)tap * CO16 + co / 16) * NB + cb) * 64 + lane) * 8) = v;
     }
 }
 
@@ -74,11 +89,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
     // A fragments straight from the packed weight (L2-resident, shared by all
     // blocks): issued first so their latency hides behind the input staging.
     half8 wa[KS * KS];
-    const uint32_t co_a = min(co0 + half * 16 + fr, p.co - 1);
+    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * 2 + half, CO16 - 1);   // past Co: discarded
     auto load_w = [&](uint32_t cb) {
 #pragma unroll
         for (int tap = 0; tap < KS * KS; ++tap)
-            wa[tap] = *(const half8*)(p.wp + ((size_t)tap * p.co + co_a) * C32 + cb * 32 + fg * 8);
+            wa[tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * nblk + cb) * 64 + lane) * 8);
     };
     if ((uint32_t)cw < nblk) load_w(cw);
 
@@ -209,12 +224,12 @@ bool conv_nhwc_ok(uint32_t ci, uint32_t wi, uint32_t wo, uint32_t ks)
 
 size_t conv_packed_weight_bytes(uint32_t ci, uint32_t co, uint32_t ks)
 {
-    return (size_t)ks * ks * co * cv::ci32(ci) * 2;
+    return (size_t)ks * ks * ((co + 15) / 16 * 16) * cv::ci32(ci) * 2;
 }
 
 hipError_t conv_pack_weight(half_t* dst, const half_t* w, uint32_t ci, uint32_t co, uint32_t ks, hipStream_t s)
 {
-    hipLaunchKernelGGL(pack_weight_kernel, dim3(co), dim3(256), (size_t)ci * ks * ks * 2, s, dst, w, co, ci,
+    hipLaunchKernelGGL(pack_weight_kernel, dim3((co + 15) / 16 * 16), dim3(256), (size_t)ci * ks * ks * 2, s, dst, w, co, ci,
                        cv::ci32(ci), ks * ks);
     return hipGetLastError();
 }

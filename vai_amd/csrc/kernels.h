@@ -96,11 +96,11 @@ hipError_t gemm_f32_launch(const GemmParams& p, int nf, hipStream_t s);
 bool scores_fast_ok(const GemmParams& p);
 hipError_t scores_launch(const GemmParams& p, hipStream_t s);
 
-// Implicit-GEMM convolution, fp16 weights packed [tap][Co][C32].
+// Implicit-GEMM convolution, fp16 weights packed per tap in MFMA fragment order.
 struct ConvParams {
     void* out;
     const void* x;                // input [B][Ci][Hi][Wi], fp16 or fp32
-    const half_t_storage* wp;     // packed weight [k*k][Co][C32]
+    const half_t_storage* wp;     // packed weight [k*k][Co/16][C32/32][64 lanes][8]
     const void* bias;             // fp16 [Co] or null
     const void* scale;            // fp16 [Co] or null
     const void* residual;         // [B][Co][Ho][Wo] (residual_dtype) or null

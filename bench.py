@@ -144,6 +144,42 @@ def build_cases(capi, stream, which):
         cases["3"] = Case("prefill gate/up X[2048,3072] W[2x8192,3072] fp16, SiLU(g)*u fused, fp32 out",
                           "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn, kern, flops, 180355072, "f16", "3")
 
+    if "ffn" in which:   # the whole gated MLP block at config 3's shape (Llama-3.2-3B FFN), fp16 between nodes
+        wg = f16(rng.standard_normal((3072, 8192)) * 0.02).T
+        wu = f16(rng.standard_normal((3072, 8192)) * 0.02).T
+        w1 = D(np.ascontiguousarray(np.concatenate([wg, wu], 0)))
+        w2 = D(f16(rng.standard_normal((8192, 3072)) * 0.02).T.copy())
+        x = D(f16(rng.standard_normal((2048, 3072))))
+        res = D(f16(rng.standard_normal((2048, 3072))))
+        hid = capi.DeviceArray((2048, 8192), np.float16)
+        y = capi.DeviceArray((2048, 3072), np.float16)
+        a1 = capi.linear_args(hid, x, w1, gated=True, gate_epi="SILU")
+        a2 = capi.linear_args(y, hid, w2, None, res)
+        keep = [w1, w2, x, res, hid, y, a1, a2]
+        for a in (a1, a2):
+            packed = capi.linear_pack_weight(a, stream.ptr)
+            if packed is not None:
+                a.packed_weight = packed.ptr
+                keep.append(packed)
+            need = capi.linear_workspace_size(a)
+            if need:
+                wsp = capi.DeviceArray((need,), np.uint8)
+                keep.append(wsp)
+                a.workspace, a.workspace_bytes = wsp.ptr, wsp.nbytes
+        stream.synchronize()
+        r1, r2 = ctypes.byref(a1), ctypes.byref(a2)
+
+        def fnf(i):
+            capi.check(lib.vai_linear_launch(r1, stream.ptr), "ffn gate/value")
+            capi.check(lib.vai_linear_launch(r2, stream.ptr), "ffn out")
+        fnf.keep = keep
+        flops = 2 * 2048 * 3072 * 16384 + 2 * 2048 * 8192 * 3072
+        kern = capi.linear_plan(a1)[0] + " + " + capi.linear_plan(a2)[0]
+        cases["ffn"] = Case("gated MLP block X[2048,3072] -> SiLU(g)*u [2048,8192] -> out [2048,3072] + residual, fp16",
+                            "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnf, kern, flops,
+                            2048 * 3072 * 2 + 16384 * 3072 * 2 + 2048 * 8192 * 2 * 2 + 3072 * 8192 * 2 + 2048 * 3072 * 2 * 2,
+                            "f16", "ffn")
+
     if "4" in which:   # attention scores; rotate S outputs past the MALL
         q = D(f16(rng.standard_normal((8, 1024, 256))))
         k = D(f16(rng.standard_normal((8, 1024, 256))))

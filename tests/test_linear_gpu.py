@@ -297,3 +297,36 @@ def test_linear_f32_small(gpu, m, k, n, bias, res, order, odt, epi):
     assert_close(got.astype(np.float32), want.astype(np.float32), tol)
     again = run_linear(gpu, x, w, b, r, out_dtype=odt, epi=epi, order=order)
     np.testing.assert_array_equal(again, got)
+
+
+@pytest.mark.parametrize("m, k, n, odt, epi, residual, bias, splits", [
+    (2048, 8192, 3072, np.float16, "NONE", True, False, 2),    # the FFN down projection: 96 tiles
+    (1000, 2048, 1000, np.float32, "GELU_TANH", False, True, 8),   # 16 tiles, M and N tails
+    (512, 4096, 2304, np.float32, "SILU", True, True, 8),      # [M,N] residual; 14 splits do not divide K
+])
+def test_linear_packed_split_k(gpu, m, k, n, odt, epi, residual, bias, splits):
+    """Packed-weight GEMMs with too few 256x256 tiles split K into units
+    that fill the CUs; the partial planes go through the reduce pass, which
+    applies bias, activation and residual. vs the oracle on sampled rows."""
+    rng = np.random.default_rng(2)
+    w = draw(normal((n, k), 0.02), rng, np.float16)
+    b = draw(normal((n,), 0.05), rng, np.float16) if bias else None
+    x = draw((m, k), rng, np.float16)
+    r = draw((m, n), rng, odt) if residual else None
+    D = gpu.DeviceArray.from_numpy
+    dx, dw = D(x), D(w)
+    out = gpu.DeviceArray((m, n), odt)
+    db, dr = (D(b) if bias else None), (D(r) if residual else None)
+    a = gpu.linear_args(out, dx, dw, db, dr, epi=epi)
+    packed = gpu.linear_pack_weight(a)
+    a.packed_weight = packed.ptr
+    name, got_splits = gpu.linear_plan(a)
+    assert name == "tile_f16_256x256_packed" and got_splits == splits, (name, got_splits)
+    got = gpu.linear(out, dx, dw, db, dr, packed=packed, epi=epi).numpy()
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(m - 4, m),
+                                     np.random.default_rng(1).choice(m, 24, replace=False)]))
+    want = oracle.linear(x[rows], w, b, r[rows] if residual else None, epi=epi, out_dtype=odt, stage="tile")
+    tol = FP16 if odt == np.float16 else TRANS
+    assert_close(got[rows].astype(np.float32), want.astype(np.float32), tol)
+    again = gpu.linear(out, dx, dw, db, dr, packed=packed, epi=epi).numpy()
+    np.testing.assert_array_equal(again, got)

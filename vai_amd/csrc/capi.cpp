@@ -74,12 +74,25 @@ LinearPlan plan_linear(const vai_linear_args* a)
         GemmParams g{};
         g.a_dtype = a->i_dtype; g.b_dtype = a->w_dtype; g.M = M; g.N = N; g.K = K; g.H = a->gated ? N / 2 : 0;
         g.A = a->in; g.B = a->weight; g.splits = 1; g.batch = 1;
-        if (a->split_size == 0 && a->packed_weight && gemm_packed_ok(g, a->gated)) {
-            p.kind = LinearPlan::PackedTile;
-            p.splits = 1;
-            p.split_size = K;
-            p.workspace = 0;
-            return p;
+        if (a->split_size == 0 && a->packed_weight) {
+            // Fewer 256x256 tiles than half the CUs (a down projection: M=2048,
+            // N=3072 is 96 tiles): split K so the units fill the chip, the
+            // partial planes summed by the reduce pass.
+            const uint32_t tiles = tiles_of(M, a->gated ? N / 2 : N, 256, a->gated ? 128 : 256);
+            uint32_t splits = 1;
+            if (!a->gated && tiles < kCUs / 2) {
+                splits = std::max<uint32_t>(1, std::min<uint32_t>(kCUs / tiles, K / 256));
+                while (splits > 1 && K % (splits * 128) != 0) --splits;
+            }
+            g.splits = splits;
+            if (gemm_packed_ok(g, a->gated)) {
+                p.kind = LinearPlan::PackedTile;
+                p.splits = splits;
+                p.split_size = K / splits;
+                p.workspace = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+                return p;
+            }
+            g.splits = 1;
         }
         // fp32 problems with fewer 64x64 tiles than CUs: one launch over the
         // full K with a CU-filling tile count, instead of split-K + reduce
@@ -231,7 +244,14 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
     g.H = a->gated ? a->N / 2 : 0;
     if (p.splits > 1) { g.C = a->workspace; g.c_dtype = VAI_DTYPE_F32; }
     else { g.C = a->out; g.c_dtype = a->o_dtype; }
-    if (p.kind == LinearPlan::PackedTile) return hip_status(gemm_packed_launch(g, a->packed_weight, a->gated != 0, s));
+    if (p.kind == LinearPlan::PackedTile) {
+        hipError_t e = gemm_packed_launch(g, a->packed_weight, a->gated != 0, s);
+        if (e != hipSuccess || p.splits == 1) return hip_status(e);
+        return hip_status(linear_reduce_launch(a->out, a->o_dtype, (const float*)a->workspace, p.splits,
+                                               (size_t)a->M * a->N, a->bias, a->b_dtype, a->bias_repeat, a->residual,
+                                               a->residual_repeat, a->epilogue, a->residual_order, a->scalar_scale, 0,
+                                               0, a->N, s));
+    }
     if (p.kind == LinearPlan::BigTile) return hip_status(gemm_big_launch(g, a->gated != 0, s));
     if (p.kind == LinearPlan::F32Small) return hip_status(gemm_f32_launch(g, (int)(p.bn / 16), s));
     hipError_t e = gemm_launch(g, a->gated ? BKind::Gated : BKind::Dense,

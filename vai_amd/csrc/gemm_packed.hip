@@ -256,14 +256,28 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
     const uint32_t M = p.M, K = p.K, G = gridDim.x;
     const TileOrder order = TileOrder::make((M + BM - 1) / BM, GATED ? (p.H + 127) / 128 : (p.N + BN - 1) / BN, G);
     const uint32_t total = order.tiles_m * order.tiles_n;
-    const int ktiles = (int)(K / BK);   // even, >= 4
+    // Work units: (tile, K split). With p.splits = S > 1 (not gated) unit
+    // U covers tile U % total over K steps [s*ktiles, (s+1)*ktiles), s =
+    // U / total, and writes its raw fp32 sums to partial plane s at p.C; a
+    // reduce pass applies the epilogue.
+    const uint32_t S = GATED ? 1u : p.splits, units = total * S;
+    const int ktiles = (int)(K / S / BK);   // per unit: even, >= 4
     // (a division expands to VALU code: read it back as the scalar it is)
-    const int my_tiles = __builtin_amdgcn_readfirstlane((int)((total - blockIdx.x + G - 1) / G));
+    const int my_tiles = __builtin_amdgcn_readfirstlane((int)((units - blockIdx.x + G - 1) / G));
+    GemmParams up = p;   // the parameters a unit's epilogue sees
+    if (S > 1) {
+        up.bias = nullptr;
+        up.residual = nullptr;
+        up.epilogue = 0;
+        up.scalar_scale = 1.f;
+        up.c_dtype = DT_F32;
+    }
 
-    // A stream position: the tile (tm, tn) and K step kt of a stage. The
-    // stages a workgroup runs are its tiles' K steps back to back; copies past
-    // the last stage repeat it (harmless, and the copy counts stay fixed).
-    struct Pos { uint32_t tm, tn; int kt; };
+    // A stream position: the unit's tile (tm, tn), its first K step kb and
+    // the K step kt within the unit. The stages a workgroup runs are its
+    // units' K steps back to back; copies past the last stage repeat it
+    // (harmless, and the copy counts stay fixed).
+    struct Pos { uint32_t tm, tn; int kt; int kb; uint32_t split; };
 
     // A copies: copy i of wave w fills slab slots [(w*A_LOADS + i)*64, +64);
     // slot s holds row s/CH, physical chunk s%CH = logical chunk ^ swizzle.
@@ -286,7 +300,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LDS_AS void*)(dst + i * 1024), 16, (int)voff[i],
-                                                     (int)(at.kt * BK * 2), 0, 0);
+                                                     (int)((at.kb + at.kt) * BK * 2), 0, 0);
     };
 
     // A fragments of substep ks of stage g: rows i*32 + fr share the swizzle
@@ -316,11 +330,12 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
     half8 fa[2][8];
     half8 fb0[4][2], fb1[4][2];
 
-    auto load_b = [&](struct Pos at, half8 (&fb)[4][2], int q) __attribute__((always_inline)) {
+    auto load_b = [&](struct Pos at, half8 (&fb)[4][2], int qq) __attribute__((always_inline)) {
         const char* base =
-            (const char*)wp + (size_t)(at.tn * 8 + wave * 2) * blk + (size_t)at.kt * 4096 + q * 1024 + lane * 16;
+            (const char*)wp + (size_t)(at.tn * 8 + wave * 2) * blk + (size_t)(at.kb + at.kt) * 4096 + qq * 1024 +
+            lane * 16;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) fb[q][j] = *(const half8*)(base + j * blk);
+        for (int j = 0; j < 2; ++j) fb[qq][j] = *(const half8*)(base + j * blk);
     };
 
     // Position d stages after K step kt of the current tile.
@@ -380,12 +395,15 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         });
     };
 
-    // Tile r of this workgroup (uniform: the divisions in TileOrder expand to
-    // VALU code, so the result is read back as a scalar).
+    // Unit r of this workgroup (uniform: the divisions expand to VALU code,
+    // so the results are read back as scalars).
     auto tile_pos = [&](int r) __attribute__((always_inline)) {
+        const uint32_t U = blockIdx.x + (uint32_t)r * G;
+        const uint32_t split = (uint32_t)__builtin_amdgcn_readfirstlane(U / total);
         uint32_t tm, tn;
-        order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
-        return Pos{(uint32_t)__builtin_amdgcn_readfirstlane(tm), (uint32_t)__builtin_amdgcn_readfirstlane(tn), 0};
+        order.of(U - split * total, tm, tn);
+        return Pos{(uint32_t)__builtin_amdgcn_readfirstlane(tm), (uint32_t)__builtin_amdgcn_readfirstlane(tn), 0,
+                   (int)split * ktiles, split};
     };
 
     // Prologue. The issue order A(0), A(1), B(0), A(2) is the order the loop
@@ -393,11 +411,11 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
     // g), so the compiler's waits for B registers come out the same on entry
     // and on the back edge.
     Pos here = tile_pos(0);
-    issue_a(0, Pos{here.tm, here.tn, 0});
-    issue_a(1, Pos{here.tm, here.tn, 1});
+    issue_a(0, Pos{here.tm, here.tn, 0, here.kb, here.split});
+    issue_a(1, Pos{here.tm, here.tn, 1, here.kb, here.split});
 #pragma unroll
     for (int q = 0; q < 4; ++q) load_b(here, fb0, q);
-    issue_a(2, Pos{here.tm, here.tn, 2});
+    issue_a(2, Pos{here.tm, here.tn, 2, here.kb, here.split});
     pk_wait_vmcnt<(SLOTS - 1) * A_LOADS + B_LOADS>();
     __builtin_amdgcn_s_barrier();
     read_a(0, 0, fa[0]);
@@ -407,8 +425,9 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         here = tile_pos(r);
         const bool has_next = r + 1 < my_tiles;
         const Pos next = has_next ? tile_pos(r + 1) : here;
+        if (S > 1) up.C = (float*)p.C + (size_t)here.split * M * p.N;
         float cb[2];
-        pk_col_bias<GATED>(p, here.tn, wave, fr, cb);
+        pk_col_bias<GATED>(up, here.tn, wave, fr, cb);
         float16v acc[8][2];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -431,7 +450,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         here.kt = ktiles - 1;
         stage(g, here, next, has_next, acc, fb1, fb0);
         ++g;
-        pk_store<GATED>(p, acc, cb, here.tm, here.tn, wave, fr, fk);
+        pk_store<GATED>(up, acc, cb, here.tm, here.tn, wave, fr, fk);
     }
     pk_wait_vmcnt<0>();   // the clamped copies land before the workgroup retires
 }
@@ -441,9 +460,11 @@ bool gemm_packed_ok(const GemmParams& p, bool gated)
     const uint32_t ncols = gated ? 2 * p.H : p.N;
     // K % 128: the stage loop runs two stages per trip; K >= 256: the copies
     // run at most one tile ahead
-    return p.a_dtype == DT_F16 && p.b_dtype == DT_F16 && p.K % 128 == 0 && p.K >= 256 && p.splits == 1 &&
-           p.batch == 1 && (size_t)p.M * p.K * 2 < (1u << 31) &&
-           (size_t)((p.M + 255) / 256) * ((ncols + 255) / 256) >= 128;
+    // (split-K, not gated: K / splits obeys the same rules)
+    const uint32_t S = p.splits ? p.splits : 1;
+    if (S > 1 && (gated || p.K % (S * 128) != 0 || p.K / S < 256)) return false;
+    return p.a_dtype == DT_F16 && p.b_dtype == DT_F16 && p.K % 128 == 0 && p.K >= 256 && p.batch == 1 &&
+           (size_t)p.M * p.K * 2 < (1u << 31) && (size_t)((p.M + 255) / 256) * ((ncols + 255) / 256) * S >= 128;
 }
 
 hipError_t gemm_packed_launch(const GemmParams& p, const void* packed, bool gated, hipStream_t s)
@@ -465,7 +486,8 @@ hipError_t gemm_packed_launch(const GemmParams& p, const void* packed, bool gate
         hipError_t e = hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
     }
-    const uint32_t grid = std::min<uint32_t>(tiles_m * tiles_n, (uint32_t)cus[dev]);
+    const uint32_t units = tiles_m * tiles_n * (gated ? 1u : std::max<uint32_t>(p.splits, 1));
+    const uint32_t grid = std::min<uint32_t>(units, (uint32_t)cus[dev]);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), pk::LDS_BYTES, s, p, (const half_t*)packed);
     return hipGetLastError();
 }

@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,ffn,5/k1s1,5/k3s2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--repeats", type=int, default=3)
@@ -212,6 +212,29 @@ def build_cases(capi, stream, which):
         flops = 2 * 6400 * 128 * 1152
         cases["5"] = Case("YOLOX-s 3x3 conv in[1,128,80,80] W[128,128,3,3] fp16 +bias SiLU, fp32 out",
                           "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn5, "conv_kernel<3> (implicit GEMM, packed weight)", flops, 5210368, "f16", "5")
+    for key, (ci, co, ks, st, hw) in {"5/k1s1": (256, 128, 1, 1, 40), "5/k3s2": (128, 256, 3, 2, 80)}.items():
+        if key not in which:
+            continue
+        # the other YOLOX-s conv plans: a CSP pointwise conv and the 3x3 stride-2 downsample
+        wt = D(f16(rng.standard_normal((co, ci, ks, ks)) * 0.03))
+        bias = D(f16(rng.standard_normal(co) * 0.02))
+        x = D(f16(rng.uniform(-1, 1, (1, ci, hw, hw))))
+        ho = (hw - 1) // st + 1
+        out = capi.DeviceArray((1, co, ho, ho), np.float32)
+        ac = capi.conv2d_args(out, x, wt, bias, stride=st, epi="SILU")
+        wsc = capi.conv2d_pack_weight(ac, stream.ptr)
+        stream.synchronize()
+        ac.packed_weight = wsc.ptr if wsc is not None else None
+        rc = ctypes.byref(ac)
+
+        def fnc(i, rc=rc):
+            capi.check(lib.vai_conv2d_launch(rc, stream.ptr), "conv")
+        fnc.keep = [wt, bias, x, out, ac, wsc]
+        flops = 2 * ho * ho * co * ci * ks * ks
+        byts = ci * hw * hw * 2 + co * ci * ks * ks * 2 + co * 2 + co * ho * ho * 4
+        cases[key] = Case(f"YOLOX-s {ks}x{ks}/s{st} conv in[1,{ci},{hw},{hw}] W[{co},{ci},{ks},{ks}] fp16 +bias SiLU, fp32 out",
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnc, f"conv_kernel<{ks}> (implicit GEMM, packed weight)",
+                          flops, byts, "f16", key)
     return cases
 
 

@@ -49,6 +49,24 @@ def test_conv(gpu, ci, co, ks, stride, hw, batch, epi, dt):
     assert_close(got, want, TRANS if dt == np.float32 else FP16)
 
 
+@pytest.mark.parametrize("ci, co, ks, stride, hw", [(256, 128, 1, 1, 40), (128, 256, 3, 2, 80)])
+def test_conv_yolox_plans(gpu, ci, co, ks, stride, hw):
+    """The other YOLOX-s conv plans at their real shapes: a CSP pointwise
+    conv (conv-k1s1-gemm.comp) and the 3x3 stride-2 downsample
+    (conv-k3s2-gemm.comp), fp16, bias + SiLU, packed weight."""
+    rng = np.random.default_rng(5)
+    w = draw(normal((co, ci, ks, ks), 0.03), rng, np.float16)
+    b = draw(normal((co,), 0.02), rng, np.float16)
+    x = draw(uniform((1, ci, hw, hw), -1, 1), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    ho = (hw - 1) // stride + 1
+    out = gpu.DeviceArray((1, co, ho, ho), np.float32)
+    a = gpu.conv2d_args(out, D(x), D(w), D(b), stride=stride, epi="SILU")
+    packed = gpu.conv2d_pack_weight(a)
+    got = gpu.conv2d(out, D(x), D(w), D(b), stride=stride, epi="SILU", packed=packed).numpy()
+    assert_close(got, oracle.conv2d(x, w, b, stride=stride, epi="SILU"), FP16)
+
+
 @pytest.mark.parametrize("order", [0, 1])
 def test_conv_scale_residual(gpu, order):
     rng = np.random.default_rng(0)

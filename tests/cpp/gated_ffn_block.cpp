@@ -1,10 +1,14 @@
 // gated_ffn_block.cpp -- the full gated MLP block, as a model net uses it:
 // a NeuralNet holding vai::group::GatedFeedForward, wired with the flow DSL.
 //
-//   gated_ffn_block <dir> <M> <K> <H> <N> <residual 0|1> <act silu|gelu_tanh> <odt f32|f16>
+//   gated_ffn_block <dir> <M> <K> <H> <N> <residual 0|1> <act silu|gelu_tanh> <odt f32|f16> [checkpoint dir]
 //
 // reads <dir>/x.f32 [M,K], <dir>/w1.f32 [2H,K] (gate rows, then value rows),
-// <dir>/w2.f32 [N,H], and with residual <dir>/r.f32 [M,N]; weights are fp16
+// <dir>/w2.f32 [N,H], and with residual <dir>/r.f32 [M,N]. With a checkpoint
+// folder the weights come from its .safetensors shards instead, under the
+// Llama names mlp.gate_proj.weight [H,K], mlp.up_proj.weight [H,K] and
+// mlp.down_proj.weight [N,H], the gate/value weight being concat(gate, up)
+// as the reference's meta-weights.h:53-57 builds it. Weights are fp16
 // (the net default); x, the residual and the activations between the nodes
 // use <odt> (the net's output default). Runs the block twice (record, then replay), writes
 // <dir>/y.f32 [M,N] and prints the two Linear plans and the record/submit
@@ -20,6 +24,7 @@
 #include "graph-flow.h"
 #include "groups.h"
 #include "nodes.h"
+#include "safetensors.h"
 
 namespace {
 
@@ -56,8 +61,8 @@ struct Block : vai::NeuralNet
 
 int main(int argc, char** argv)
 {
-    if (argc != 9) {
-        std::fprintf(stderr, "usage: %s <dir> <M> <K> <H> <N> <residual> <silu|gelu_tanh> <f32|f16>\n", argv[0]);
+    if (argc != 9 && argc != 10) {
+        std::fprintf(stderr, "usage: %s <dir> <M> <K> <H> <N> <residual> <silu|gelu_tanh> <f32|f16> [ckpt]\n", argv[0]);
         return 2;
     }
     const std::string dir = argv[1];
@@ -67,10 +72,20 @@ int main(int argc, char** argv)
     const vai::Dtype odt = std::strcmp(argv[8], "f16") == 0 ? vai::Dtype::Fp16 : vai::Dtype::Fp32;
     try {
         Block net(K, H, N, residual, act, odt);
-        net.ffn.gateValue["weight"] = vai::Tensor({2 * H, K}, vai::Dtype::Fp16);
-        net.ffn.gateValue["weight"].setFloats(readFloats(dir + "/w1.f32", size_t(2) * H * K));
-        net.ffn.out["weight"] = vai::Tensor({N, H}, vai::Dtype::Fp16);
-        net.ffn.out["weight"].setFloats(readFloats(dir + "/w2.f32", size_t(N) * H));
+        if (argc == 10) {
+            const vai::Checkpoint ck(argv[9]);
+            const vai::Tensor gate = vai::loadTensor(ck["mlp.gate_proj.weight"], vai::Dtype::Fp16);
+            const vai::Tensor up = vai::loadTensor(ck["mlp.up_proj.weight"], vai::Dtype::Fp16);
+            if (!gate.isShapeOf({H, K}) || !up.isShapeOf({H, K})) throw std::runtime_error("gate/up shape");
+            net.ffn.gateValue["weight"] = gate.concat({up});
+            net.ffn.out["weight"] = vai::loadTensor(ck["mlp.down_proj.weight"], vai::Dtype::Fp16);
+            if (!net.ffn.out["weight"].isShapeOf({N, H})) throw std::runtime_error("down shape");
+        } else {
+            net.ffn.gateValue["weight"] = vai::Tensor({2 * H, K}, vai::Dtype::Fp16);
+            net.ffn.gateValue["weight"].setFloats(readFloats(dir + "/w1.f32", size_t(2) * H * K));
+            net.ffn.out["weight"] = vai::Tensor({N, H}, vai::Dtype::Fp16);
+            net.ffn.out["weight"].setFloats(readFloats(dir + "/w2.f32", size_t(N) * H));
+        }
 
         vai::Tensor x({M, K}, odt);
         x.setFloats(readFloats(dir + "/x.f32", size_t(M) * K));

@@ -96,3 +96,37 @@ def test_gated_ffn_block_from_cpp(gpu, tmp_path, m, k, h, n, residual, act, odt,
 
 def test_cpp_block_program_is_built():
     assert os.access(BLOCK, os.X_OK), "tests/cpp/_bin/gated_ffn_block missing: run __graft_entry__.build()"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_gated_ffn_block_from_checkpoint(gpu, tmp_path, dtype):
+    """Weights ingested from a sharded .safetensors checkpoint (Llama MLP
+    names, bf16 or fp16 as published) into the GatedFeedForward block, then
+    run on the GPU; vs the oracle on the weights as the engine stores them
+    (fp16)."""
+    import torch
+    from safetensors.torch import save_file
+    m, k, h, n = 256, 512, 768, 384
+    rng = np.random.default_rng(4)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    g = torch.from_numpy(rng.standard_normal((h, k)).astype(np.float32) * 0.05).to(tdt)
+    u = torch.from_numpy(rng.standard_normal((h, k)).astype(np.float32) * 0.05).to(tdt)
+    dn = torch.from_numpy(rng.standard_normal((n, h)).astype(np.float32) * 0.05).to(tdt)
+    ck = tmp_path / "ckpt"
+    ck.mkdir()
+    save_file({"mlp.gate_proj.weight": g, "mlp.up_proj.weight": u}, str(ck / "model-00001-of-00002.safetensors"))
+    save_file({"mlp.down_proj.weight": dn}, str(ck / "model-00002-of-00002.safetensors"))
+    x = draw((m, k), rng, np.float16)
+    x.astype(np.float32).tofile(tmp_path / "x.f32")
+    args = [BLOCK, str(tmp_path), str(m), str(k), str(h), str(n), "0", "silu", "f16", str(ck)]
+    print(" ".join(args[2:]), flush=True)
+    p = subprocess.run(args, capture_output=True, text=True, timeout=100)
+    assert p.returncode == 0, p.stderr
+    got = np.fromfile(tmp_path / "y.f32", np.float32).reshape(m, n)
+    # the engine holds the weights as fp16: bf16 values round to nearest even
+    as16 = lambda t: t.to(torch.float32).numpy().astype(np.float16)
+    w1 = np.concatenate([as16(g), as16(u)], 0)
+    hid = oracle.gated_mul(oracle.linear(x, w1, stage="tile"), epi="SILU", out_dtype=np.float16)
+    want = oracle.linear(hid, as16(dn), out_dtype=np.float16, stage="tile")
+    assert_close(got, want.astype(np.float32), FP16)

@@ -179,6 +179,31 @@ typedef struct {
 vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Attention: O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h/g,j,:] + mask)
+ * V[b,h/g,j,:], g = Hq/Hkv, with the mask rule of vai_attn_scores_launch
+ * (causal, span). fp32 softmax statistics and accumulation; P is rounded to
+ * fp16 for the P.V product. Q [batch,Hq,Tq,D], K/V [batch,Hkv,Tkv,D] fp16,
+ * D in {64, 128, 256}; O [batch,Hq,Tq,D] in o_dtype (f32 or f16). A query
+ * with no visible key gives zeros. Replaces the flash-attention dispatch of
+ * the reference's Attention node (/root/reference/vai/nodes/attention.h:
+ * 979-1304, shaders/attention-fa.comp) for the no-cache case.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    void* out;
+    const void* q;
+    const void* k;
+    const void* v;
+    int32_t o_dtype;
+    int32_t i_dtype;              /* VAI_DTYPE_F16 */
+    uint32_t batch, hq, hkv, tq, tkv, head_dim;
+    float scale;                  /* 0: 1/sqrt(head_dim), as attention.h:1254 */
+    uint32_t causal;
+    uint32_t span;
+} vai_attention_args;
+
+vai_status vai_attention_launch(const vai_attention_args* args, vai_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Device memory and streams: what the host side (vai::Tensor's pooled
  * buffers, the reference's eva::Buffer role) and the tests use.
  * ------------------------------------------------------------------------- */

@@ -165,5 +165,26 @@ def attn_scores(q, k, *, scale=None, causal=True, span=0):
     return out
 
 
+def attention(q, k, v, *, scale=None, causal=True, span=0, out_dtype=np.float32):
+    """O = softmax(S) V per query row, S = attn_scores(q, k) (the mask's
+    -inf entries drop out), in float64 from the fp16 operands; a row with no
+    visible key gives 0. The fused pass of attention-fa.comp (scores at
+    :581-591, online softmax, P.V), /root/reference/vai/shaders/."""
+    q, k, v = _c(q), _c(k), _c(v)
+    S = attn_scores(q, k, scale=scale, causal=causal, span=span).astype(np.float64)
+    Hq, Tq, D = q.shape[-3:]
+    Hkv, Tkv, _ = k.shape[-3:]
+    g = Hq // Hkv
+    vv = np.repeat(v.astype(np.float64).reshape((-1, Hkv, Tkv, D)), g, axis=1).reshape(q.shape[:-2] + (Tkv, D))
+    finite = np.isfinite(S)
+    m = np.where(finite, S, -np.inf).max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    P = np.where(finite, np.exp(S - m), 0.0)
+    l = P.sum(axis=-1, keepdims=True)
+    O = np.einsum("...ij,...jd->...id", P, vv)
+    O = np.where(l > 0, O / np.where(l > 0, l, 1.0), 0.0)
+    return O.astype(out_dtype)
+
+
 def num_threads():
     return lib().orc_num_threads()

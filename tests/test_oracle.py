@@ -229,3 +229,45 @@ def test_scores_vs_float64(hq, hkv, tq, tkv, d, causal, span):
     assert np.array_equal(np.isneginf(got), np.isneginf(s))
     fin = ~np.isneginf(s)
     np.testing.assert_allclose(got[fin], s[fin], rtol=1e-5, atol=1e-5)
+
+
+def _attn_inputs(rng, hq, hkv, tq, tkv, d):
+    q = rng.standard_normal((1, hq, tq, d)).astype(np.float16)
+    k = rng.standard_normal((1, hkv, tkv, d)).astype(np.float16)
+    v = rng.standard_normal((1, hkv, tkv, d)).astype(np.float16)
+    return q, k, v
+
+
+def test_attention_oracle_pins():
+    """oracle.attention composes the pinned scores with softmax and P.V;
+    these properties fail for a dropped normalisation, a reversed mask or a
+    transposed V."""
+    rng = np.random.default_rng(0)
+    q, k, v = _attn_inputs(rng, 2, 1, 5, 7, 8)
+    # V of ones: every row with a visible key returns exactly 1
+    o = oracle.attention(q, k, np.ones_like(v), causal=True, out_dtype=np.float64)
+    np.testing.assert_allclose(o, 1.0, rtol=1e-12)
+    # V = identity rows (Tkv = D): O is the softmax matrix itself
+    q2, k2, _ = _attn_inputs(rng, 1, 1, 6, 8, 8)
+    eye = np.eye(8, dtype=np.float16)[None, None]
+    o = oracle.attention(q2, k2, eye, causal=False, out_dtype=np.float64)[0, 0]
+    s = q2[0, 0].astype(np.float64) @ k2[0, 0].astype(np.float64).T / np.sqrt(8)
+    p = np.exp(s - s.max(1, keepdims=True))
+    np.testing.assert_allclose(o, p / p.sum(1, keepdims=True), rtol=1e-6)
+    # causal with Tq = Tkv: query 0 sees key 0 alone, so O[0] = V[0]; the
+    # last query sees every key
+    q3, k3, v3 = _attn_inputs(rng, 1, 1, 6, 6, 8)
+    o = oracle.attention(q3, k3, v3, causal=True, out_dtype=np.float64)[0, 0]
+    np.testing.assert_array_equal(o[0], v3[0, 0, 0].astype(np.float64))
+    full = oracle.attention(q3, k3, v3, causal=False, out_dtype=np.float64)[0, 0]
+    np.testing.assert_allclose(o[-1], full[-1], rtol=1e-12)
+    # GQA: two query heads over one K/V head equal two single-head calls
+    qa, kb, vb = _attn_inputs(rng, 2, 1, 4, 4, 8)
+    both = oracle.attention(qa, kb, vb, causal=True, out_dtype=np.float64)
+    for h in range(2):
+        one = oracle.attention(qa[:, h:h + 1], kb, vb, causal=True, out_dtype=np.float64)
+        np.testing.assert_allclose(both[:, h:h + 1], one, rtol=1e-12)
+    # Tq > Tkv under the causal rule: the first queries see no key and give 0
+    q4, k4, v4 = _attn_inputs(rng, 1, 1, 5, 3, 8)
+    o = oracle.attention(q4, k4, v4, causal=True, out_dtype=np.float64)[0, 0]
+    np.testing.assert_array_equal(o[:2], 0.0)

@@ -21,7 +21,7 @@ EXPORTS = [
     "vai_linear_launch", "vai_linear_workspace_size", "vai_linear_plan", "vai_gated_mul_launch",
     "vai_linear_packed_weight_size", "vai_linear_pack_weight",
     "vai_conv2d_launch", "vai_conv2d_workspace_size", "vai_conv2d_packed_weight_size", "vai_conv2d_pack_weight",
-    "vai_attn_scores_launch",
+    "vai_attn_scores_launch", "vai_attention_launch",
     "vai_device_count", "vai_set_device", "vai_malloc", "vai_free", "vai_memcpy_h2d", "vai_memcpy_d2h",
     "vai_memcpy_d2d", "vai_memset", "vai_stream_create", "vai_stream_destroy", "vai_stream_sync",
     "vai_device_sync", "vai_status_string", "vai_event_create", "vai_event_destroy", "vai_event_record",
@@ -69,6 +69,16 @@ class AttnScoresArgs(ctypes.Structure):
     ]
 
 
+class AttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("out", ctypes.c_void_p), ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o_dtype", ctypes.c_int32), ("i_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_uint32), ("hq", ctypes.c_uint32), ("hkv", ctypes.c_uint32),
+        ("tq", ctypes.c_uint32), ("tkv", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+        ("scale", ctypes.c_float), ("causal", ctypes.c_uint32), ("span", ctypes.c_uint32),
+    ]
+
+
 class VaiError(RuntimeError):
     pass
 
@@ -98,6 +108,7 @@ def lib():
         L.vai_conv2d_packed_weight_size.restype = sz
         L.vai_conv2d_pack_weight.argtypes = [ctypes.POINTER(Conv2dArgs), vp, sz, vp]
         L.vai_attn_scores_launch.argtypes = [ctypes.POINTER(AttnScoresArgs), vp]
+        L.vai_attention_launch.argtypes = [ctypes.POINTER(AttentionArgs), vp]
         L.vai_malloc.argtypes = [ctypes.POINTER(vp), sz]
         L.vai_free.argtypes = [vp]
         L.vai_memcpy_h2d.argtypes = [vp, vp, sz, vp]
@@ -325,6 +336,26 @@ def attn_scores(scores, q, k, stream=None, **kw):
     a = attn_scores_args(scores, q, k, **kw)
     check(lib().vai_attn_scores_launch(ctypes.byref(a), stream), "vai_attn_scores_launch")
     return scores
+
+
+def attention_args(out, q, k, v, *, scale=None, causal=True, span=0):
+    Hq, Tq, D = q.shape[-3:]
+    Hkv, Tkv, _ = k.shape[-3:]
+    a = AttentionArgs()
+    a.out, a.q, a.k, a.v = out.ptr, q.ptr, k.ptr, v.ptr
+    a.o_dtype, a.i_dtype = out.code, q.code
+    a.batch = int(np.prod(q.shape[:-3]))
+    a.hq, a.hkv, a.tq, a.tkv, a.head_dim = Hq, Hkv, Tq, Tkv, D
+    a.scale = 0.0 if scale is None else float(scale)
+    a.causal = 1 if causal else 0
+    a.span = span
+    return a
+
+
+def attention(out, q, k, v, stream=None, **kw):
+    a = attention_args(out, q, k, v, **kw)
+    check(lib().vai_attention_launch(ctypes.byref(a), stream), "vai_attention_launch")
+    return out
 
 
 def synchronize():

@@ -1,0 +1,206 @@
+// attention.hip -- fused attention forward O = softmax(scale * Q K^T + mask) V
+// for fp16 Q/K/V on gfx950 (the role of /root/reference/vai/shaders/
+// attention-fa.comp: scores, online softmax and P.V in one pass; the mask
+// rule of common/causal_mask.h:25-42; the node at nodes/attention.h:979-1304).
+//
+// One workgroup (4 waves) owns 64 query rows of one head, 16 per wave, and
+// walks the key tiles (64 keys) the mask leaves visible. Per key tile:
+//  * K [64 x D] and V^T [D x 64] are staged in LDS (V transposed on the way,
+//    so a lane reads its P.V operand as two 8-byte runs);
+//  * S^T = K Q^T on v_mfma_f32_16x16x32_f16 (A = K rows from LDS, B = the
+//    wave's Q rows, held in registers for the whole walk). S^T rather than S:
+//    the output then gives lane l query row l % 16 and 16 of the tile's keys
+//    (16f + 4*(l/16) + r), which is exactly the A operand of the P.V MFMA
+//    with the keys of a 32-wide step in the order 4g + r, 16 + 4g + r; V is
+//    read in the same key order, so each product is still summed once;
+//  * online softmax per query row (running max m and sum l in fp32; row
+//    reductions are two cross-lane exchanges), exp2 with scale * log2(e)
+//    folded in;
+//  * O += P V with P rounded to fp16 (the fp16 operand of the reference's
+//    P.V stage), O in fp32 registers: D/16 fragments of 16x16.
+// The rows a lane holds in O (4*(l/16) + r) differ from its softmax row
+// (l % 16): the per-row rescale and the final 1/l move across lanes by
+// shuffle. Rows with no visible key give 0.
+#include <algorithm>
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace vai_dev {
+
+namespace fa {
+constexpr int BQ = 64, BKV = 64;
+template <int D> struct Lds {
+    static constexpr int KP = D + 8;              // K row pitch (halves): rows 16 B apart in banks
+    static constexpr int VP = BKV + 8;            // V^T row pitch (halves)
+    static constexpr int K_BYTES = BKV * KP * 2;
+    static constexpr int BYTES = K_BYTES + D * VP * 2;
+};
+}
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+template <int D>
+__global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
+{
+    using namespace fa;
+    constexpr int KP = Lds<D>::KP, VP = Lds<D>::VP, KS = D / 32, DB = D / 16;
+    extern __shared__ half8 fa_lds[];
+    half_t* ks = (half_t*)fa_lds;                              // [BKV][KP]
+    half_t* vt = ks + BKV * KP;                                // [D][VP]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const uint32_t Tq = p.tq, Tkv = p.tkv;
+    const uint32_t q0 = blockIdx.x * BQ, h = blockIdx.y, b = blockIdx.z;
+    const uint32_t hk = h / (p.hq / p.hkv);
+    const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
+    const half_t* K = (const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D;
+    const half_t* V = (const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * D;
+    const int64_t off = (int64_t)Tkv - (int64_t)Tq;   // query i sits at key position i + off
+
+    // this wave's 16 query rows as the B operand of S^T = K Q^T
+    const uint32_t qrow = q0 + wave * 16 + lr;
+    half8 qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+        qf[s] = qrow < Tq ? *(const half8*)(Q + (size_t)qrow * D + s * 32 + lg * 8) : (half8)0;
+
+    // visible key range of the whole tile
+    int64_t kend = (int64_t)Tkv;
+    if (p.causal) kend = std::min<int64_t>(kend, (int64_t)q0 + BQ - 1 + off + 1);
+    int64_t kbeg = 0;
+    if (p.span) kbeg = std::max<int64_t>(0, (int64_t)q0 + off + 1 - (int64_t)p.span);
+    kbeg = kbeg / BKV * BKV;
+
+    const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
+    const int64_t qpos = (int64_t)qrow + off;
+    float m = -__builtin_inff(), l = 0.f;
+    float4v o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) o[d] = (float4v)0.f;
+
+    for (int64_t j0 = kbeg; j0 < kend; j0 += BKV) {
+        __syncthreads();   // the previous tile's reads are done
+        // K rows -> LDS (16-byte chunks); V rows -> V^T in LDS
+        for (int c = tid; c < BKV * (D / 8); c += 256) {
+            const int r = c / (D / 8), ch = c % (D / 8);
+            const int64_t key = j0 + r;
+            half8 kv = (half8)0, vv = (half8)0;
+            if (key < (int64_t)Tkv) {
+                kv = *(const half8*)(K + (size_t)key * D + ch * 8);
+                vv = *(const half8*)(V + (size_t)key * D + ch * 8);
+            }
+            *(half8*)(ks + r * KP + ch * 8) = kv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vt[(ch * 8 + e) * VP + r] = vv[e];
+        }
+        __syncthreads();
+
+        // S^T for the 4 key blocks of 16: lane holds query row lr, keys 16f + 4lg + r
+        float4v st[4];
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            st[f] = (float4v)0.f;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const half8 ka = *(const half8*)(ks + (16 * f + lr) * KP + s * 32 + lg * 8);
+                st[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[s], st[f], 0, 0, 0);
+            }
+        }
+        // mask, scale, running max
+        float tmax = -__builtin_inff();
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t kpos = j0 + 16 * f + 4 * lg + r;
+                const bool hide = kpos >= (int64_t)Tkv || (p.causal && kpos > qpos) ||
+                                  (p.span && kpos < qpos + 1 - (int64_t)p.span);
+                const float v = hide ? -__builtin_inff() : st[f][r] * sl2;
+                st[f][r] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m, tmax);
+        const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+        float psum = 0.f;
+        half8 pa[2];
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = st[f][r] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(st[f][r] - mnew);
+                psum += e;
+                pa[f / 2][(f % 2) * 4 + r] = (half_t)e;
+            }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l = alpha * l + psum;
+        m = mnew;
+
+        // O rows 4lg + r take the rescale of their softmax row (held by lane 4lg + r)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) o[d][r] *= ar;
+        }
+        // O += P V: k-step s2 covers keys 32 s2 + {4lg + r, 16 + 4lg + r}
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const half_t* vr = vt + (d * 16 + lr) * VP + 32 * s2 + 4 * lg;
+                const half4v lo = *(const half4v*)vr, hi = *(const half4v*)(vr + 16);
+                const half8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[s2], vb, o[d], 0, 0, 0);
+            }
+    }
+
+    // O / l per row, then the store: lane holds rows 4lg + r, column d*16 + lr
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float ir = __shfl(inv, 4 * lg + r, 64);
+        const uint32_t row = q0 + wave * 16 + 4 * lg + r;
+        if (row >= Tq) continue;
+        const size_t base = (((size_t)b * p.hq + h) * Tq + row) * D + lr;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) st(p.out, p.o_dtype, base + d * 16, o[d][r] * ir);
+    }
+}
+
+bool attention_ok(const AttnParams& p)
+{
+    return (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256) && p.hq > 0 && p.hkv > 0 &&
+           p.hq % p.hkv == 0 && ((uintptr_t)p.q % 16) == 0 && ((uintptr_t)p.k % 16) == 0 &&
+           ((uintptr_t)p.v % 16) == 0;
+}
+
+template <int D>
+static hipError_t attention_launch_d(const AttnParams& p, hipStream_t s)
+{
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)attention_fwd_kernel<D>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, fa::Lds<D>::BYTES);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const dim3 grid((p.tq + fa::BQ - 1) / fa::BQ, p.hq, p.batch);
+    hipLaunchKernelGGL(attention_fwd_kernel<D>, grid, dim3(256), fa::Lds<D>::BYTES, s, p);
+    return hipGetLastError();
+}
+
+hipError_t attention_launch(const AttnParams& p, hipStream_t s)
+{
+    switch (p.head_dim) {
+    case 64: return attention_launch_d<64>(p, s);
+    case 128: return attention_launch_d<128>(p, s);
+    case 256: return attention_launch_d<256>(p, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}   // namespace vai_dev

@@ -8,6 +8,7 @@
 // takes the MFMA GEMM with the largest tile that still gives the 256 CUs at
 // least one workgroup each, and split-K when even the smallest tile leaves
 // most CUs idle and K is long.
+#include <cmath>
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <string.h>
@@ -287,6 +288,21 @@ vai_status vai_linear_pack_weight(const vai_linear_args* a, void* packed, size_t
     if (packed_bytes < need) return VAI_ERR_WORKSPACE;
     return hip_status(gemm_pack_weight(packed, a->weight, a->N, a->K, a->gated ? a->N / 2 : 0, a->gated != 0,
                                        (hipStream_t)stream));
+}
+
+vai_status vai_attention_launch(const vai_attention_args* a, vai_stream_t stream)
+{
+    if (!a || !a->out || !a->q || !a->k || !a->v) return VAI_ERR_INVALID_ARG;
+    if (a->i_dtype != VAI_DTYPE_F16 || !dtype_ok(a->o_dtype)) return VAI_ERR_DTYPE;
+    if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || a->tkv == 0 || a->hq % a->hkv != 0)
+        return VAI_ERR_SHAPE;
+    AttnParams p{};
+    p.out = a->out; p.q = a->q; p.k = a->k; p.v = a->v; p.o_dtype = a->o_dtype;
+    p.batch = a->batch; p.hq = a->hq; p.hkv = a->hkv; p.tq = a->tq; p.tkv = a->tkv; p.head_dim = a->head_dim;
+    p.scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)a->head_dim);
+    p.causal = a->causal; p.span = a->span;
+    if (!attention_ok(p)) return VAI_ERR_UNSUPPORTED;
+    return hip_status(attention_launch(p, (hipStream_t)stream));
 }
 
 vai_status vai_gated_mul_launch(void* out, int32_t o_dtype, const void* in, int32_t i_dtype, uint32_t rows,

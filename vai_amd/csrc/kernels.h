@@ -96,6 +96,20 @@ hipError_t gemm_f32_launch(const GemmParams& p, int nf, hipStream_t s);
 bool scores_fast_ok(const GemmParams& p);
 hipError_t scores_launch(const GemmParams& p, hipStream_t s);
 
+// Fused attention forward, fp16 Q/K/V [batch, heads, tokens, head_dim].
+struct AttnParams {
+    void* out;                    // [batch, hq, tq, head_dim], o_dtype
+    const void* q;
+    const void* k;
+    const void* v;
+    int o_dtype;
+    uint32_t batch, hq, hkv, tq, tkv, head_dim;
+    float scale;
+    uint32_t causal, span;
+};
+bool attention_ok(const AttnParams& p);
+hipError_t attention_launch(const AttnParams& p, hipStream_t s);
+
 // Implicit-GEMM convolution, fp16 weights packed per tap in MFMA fragment order.
 struct ConvParams {
     void* out;

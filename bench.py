@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4,5,ffn,5/k1s1,5/k3s2")
+    ap.add_argument("--configs", default="1,2,3,4,5,ffn,attn,5/k1s1,5/k3s2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--repeats", type=int, default=3)
@@ -193,6 +193,22 @@ def build_cases(capi, stream, which):
         cases["4"] = Case("attention scores Q,K[8,1024,256] fp16, S=QK^T/16 fp32 causal", "GB/s",
                           41943040 / 1e9, "hbm", HBM_PEAK_GBS, fn4, "scores_kernel<64> (64x64 tiles, DMA staging, register epilogue)", 2 * 8 * 1024 * 1024 * 256,
                           41943040, "f16", "4")
+
+    if "attn" in which:   # the whole attention at config 4's shape: scores, softmax and P.V fused
+        q = D(f16(rng.standard_normal((8, 1024, 256))))
+        k = D(f16(rng.standard_normal((8, 1024, 256))))
+        v = D(f16(rng.standard_normal((8, 1024, 256))))
+        o = capi.DeviceArray((8, 1024, 256), np.float16)
+        aa = capi.attention_args(o, q, k, v, scale=1.0 / 16, causal=True)
+        ra = ctypes.byref(aa)
+
+        def fna(i):
+            capi.check(lib.vai_attention_launch(ra, stream.ptr), "attention")
+        fna.keep = [q, k, v, o, aa]
+        flops = 4 * 8 * 256 * (1024 * 1025 // 2)   # QK^T and P.V over the visible (causal) pairs
+        cases["attn"] = Case("attention Q,K,V[8,1024,256] fp16 causal, O = softmax(QK^T/16) V fp16 (fused)", "TFLOP/s",
+                             flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fna, "attention_fwd_kernel<256>", flops,
+                             4 * 8 * 1024 * 256 * 2, "f16", "attn")
 
     if "5" in which:   # YOLOX 3x3 conv, bias + SiLU
         wt = D(f16(rng.standard_normal((128, 128, 3, 3)) * 0.03))

@@ -20,7 +20,8 @@
 //    P.V stage), O in fp32 registers: D/16 fragments of 16x16.
 // The rows a lane holds in O (4*(l/16) + r) differ from its softmax row
 // (l % 16): the per-row rescale and the final 1/l move across lanes by
-// shuffle. Rows with no visible key give 0.
+// shuffle. Rows with no visible key give 0. The next key tile's global loads
+// are issued into registers before the current tile is computed.
 #include <algorithm>
 
 #include "device_common.h"
@@ -51,7 +52,8 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const uint32_t Tq = p.tq, Tkv = p.tkv;
-    const uint32_t q0 = blockIdx.x * BQ, h = blockIdx.y, b = blockIdx.z;
+    // the longest causal walks (the last query tiles) start first
+    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * BQ, h = blockIdx.y, b = blockIdx.z;
     const uint32_t hk = h / (p.hq / p.hkv);
     const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
     const half_t* K = (const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D;
@@ -79,22 +81,46 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
 #pragma unroll
     for (int d = 0; d < DB; ++d) o[d] = (float4v)0.f;
 
+    // Key tile j0 is loaded into registers one tile ahead (its global loads
+    // fly while the tile before it is computed), then written to LDS: K
+    // rows as 16-byte chunks, V transposed. K chunk c of a thread is row
+    // c / NC, chunk c % NC (coalesced rows, conflict-free 16-byte writes). V
+    // chunks go 8 keys x 8 chunks per 64 lanes: each load instruction reads
+    // eight 128-byte row pieces, and the transposed 2-byte writes of one
+    // instruction land on consecutive keys of 8 V^T rows (one chunk per row
+    // across the lanes would put 64 lanes on two bank positions).
+    constexpr int NC = D / 8;                  // 16-byte chunks per row
+    constexpr int CPT = BKV * NC / 256;        // chunks per thread and operand
+    half8 kreg[CPT], vreg[CPT];
+    auto vmap = [&](int i, int& r, int& ch) __attribute__((always_inline)) {
+        const int slot = (tid >> 6) + 4 * i, l = tid & 63;   // slot: 64-lane group, 0 .. NC-1
+        r = (slot % 8) * 8 + l / 8;
+        ch = (slot / 8) * 8 + l % 8;
+    };
+    auto load_tile = [&](int64_t j0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * 256, r = c / NC, ch = c % NC;
+            int vr, vc;
+            vmap(i, vr, vc);
+            kreg[i] = j0 + r < (int64_t)Tkv ? *(const half8*)(K + (size_t)(j0 + r) * D + ch * 8) : (half8)0;
+            vreg[i] = j0 + vr < (int64_t)Tkv ? *(const half8*)(V + (size_t)(j0 + vr) * D + vc * 8) : (half8)0;
+        }
+    };
+    if (kbeg < kend) load_tile(kbeg);
     for (int64_t j0 = kbeg; j0 < kend; j0 += BKV) {
         __syncthreads();   // the previous tile's reads are done
-        // K rows -> LDS (16-byte chunks); V rows -> V^T in LDS
-        for (int c = tid; c < BKV * (D / 8); c += 256) {
-            const int r = c / (D / 8), ch = c % (D / 8);
-            const int64_t key = j0 + r;
-            half8 kv = (half8)0, vv = (half8)0;
-            if (key < (int64_t)Tkv) {
-                kv = *(const half8*)(K + (size_t)key * D + ch * 8);
-                vv = *(const half8*)(V + (size_t)key * D + ch * 8);
-            }
-            *(half8*)(ks + r * KP + ch * 8) = kv;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vt[(ch * 8 + e) * VP + r] = vv[e];
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * 256, r = c / NC, ch = c % NC;
+            *(half8*)(ks + r * KP + ch * 8) = kreg[i];
+            int vr, vc;
+            vmap(i, vr, vc);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vt[(vc * 8 + e) * VP + vr] = vreg[i][e];
         }
         __syncthreads();
+        if (j0 + BKV < kend) load_tile(j0 + BKV);
 
         // S^T for the 4 key blocks of 16: lane holds query row lr, keys 16f + 4lg + r
         float4v st[4];

@@ -235,9 +235,15 @@ def test_linear_packed_weight(gpu, m, k, n, gated, odt, epi, residual, bias):
         want = oracle.linear(x[rows], w, b, r, epi=epi, out_dtype=odt, stage="tile")
     tol = FP16 if odt == np.float16 else TRANS
     assert_close(got[rows].astype(np.float32), want.astype(np.float32), tol)
-    # same MFMA order as the LDS-staged kernel: bit-identical outputs
+    # same MFMA order as the LDS-staged kernel: bit-identical fp32 sums. The
+    # two epilogues may contract the activation arithmetic differently, so an
+    # fp16 output may differ by one fp16 ulp (and no more).
     ref = run_linear(gpu, x, w, b, r, out_dtype=odt, **kw)
-    diff = got != ref
+    if odt == np.float16:
+        mag = np.maximum(np.abs(got), np.abs(ref)).astype(np.float16)
+        diff = np.abs(got.astype(np.float32) - ref.astype(np.float32)) > np.spacing(mag).astype(np.float32)
+    else:
+        diff = got != ref
     if diff.any():
         # say where, and which of the two kernels the oracle sides with
         rr, cc = np.nonzero(diff)

@@ -222,6 +222,7 @@ def linear_args(out, inp, weight, bias=None, residual=None, *, epi="NONE", order
     a.gate_epilogue = EPILOGUES[gate_epi]
     if workspace is not None:
         a.workspace, a.workspace_bytes = workspace.ptr, workspace.nbytes
+    a._keep = (out, inp, weight, bias, residual, workspace)   # the buffers live as long as the args
     return a
 
 
@@ -244,6 +245,7 @@ def linear_pack_weight(args, stream=None):
         return None
     packed = DeviceArray((n,), np.uint8)
     check(lib().vai_linear_pack_weight(ctypes.byref(args), packed.ptr, packed.nbytes, stream), "linear_pack_weight")
+    check(lib().vai_stream_sync(stream), "sync")   # args' weight buffer may go once this returns
     return packed
 
 
@@ -259,8 +261,8 @@ def linear(out, inp, weight, bias=None, residual=None, stream=None, packed=None,
         ws = DeviceArray((need,), np.uint8)
         a.workspace, a.workspace_bytes = ws.ptr, ws.nbytes
     check(lib().vai_linear_launch(ctypes.byref(a), stream), "vai_linear_launch")
-    if ws is not None:
-        check(lib().vai_stream_sync(stream), "sync")
+    # wait for the kernels: the caller may drop its argument buffers on return
+    check(lib().vai_stream_sync(stream), "sync")
     return out
 
 
@@ -269,6 +271,7 @@ def gated_mul(out, inp, epi="SILU", stream=None):
     rows = int(np.prod(out.shape[:-1]))
     check(lib().vai_gated_mul_launch(out.ptr, out.code, inp.ptr, inp.code, rows, H, EPILOGUES[epi], stream),
           "vai_gated_mul_launch")
+    check(lib().vai_stream_sync(stream), "sync")   # the caller may drop its argument buffers on return
     return out
 
 
@@ -284,6 +287,7 @@ def conv2d_args(out, inp, weight, bias=None, scale=None, residual=None, *, strid
     a.o_dtype, a.i_dtype, a.w_dtype = out.code, inp.code, weight.code
     a.epilogue = EPILOGUES[epi]
     a.residual_order = RESIDUAL_ORDERS[order] if isinstance(order, str) else int(order)
+    a._keep = (out, inp, weight, bias, scale, residual)
     return a
 
 
@@ -298,6 +302,7 @@ def conv2d_pack_weight(args, stream=None):
         return None
     packed = DeviceArray((n,), np.uint8)
     check(lib().vai_conv2d_pack_weight(ctypes.byref(args), packed.ptr, packed.nbytes, stream), "pack_weight")
+    check(lib().vai_stream_sync(stream), "sync")   # args' weight buffer may go once this returns
     return packed
 
 
@@ -313,8 +318,7 @@ def conv2d(out, inp, weight, bias=None, scale=None, residual=None, stream=None, 
         ws = DeviceArray((need,), np.uint8)
         a.workspace, a.workspace_bytes = ws.ptr, ws.nbytes
     check(lib().vai_conv2d_launch(ctypes.byref(a), stream), "vai_conv2d_launch")
-    if ws is not None:
-        check(lib().vai_stream_sync(stream), "sync")
+    check(lib().vai_stream_sync(stream), "sync")   # the caller may drop its argument buffers on return
     return out
 
 
@@ -329,12 +333,14 @@ def attn_scores_args(scores, q, k, *, scale=None, causal=True, span=0):
     a.scale = float(1.0 / np.sqrt(D)) if scale is None else float(scale)
     a.causal = 1 if causal else 0
     a.span = span
+    a._keep = (scores, q, k)
     return a
 
 
 def attn_scores(scores, q, k, stream=None, **kw):
     a = attn_scores_args(scores, q, k, **kw)
     check(lib().vai_attn_scores_launch(ctypes.byref(a), stream), "vai_attn_scores_launch")
+    check(lib().vai_stream_sync(stream), "sync")   # the caller may drop its argument buffers on return
     return scores
 
 
@@ -349,12 +355,14 @@ def attention_args(out, q, k, v, *, scale=None, causal=True, span=0):
     a.scale = 0.0 if scale is None else float(scale)
     a.causal = 1 if causal else 0
     a.span = span
+    a._keep = (out, q, k, v)
     return a
 
 
 def attention(out, q, k, v, stream=None, **kw):
     a = attention_args(out, q, k, v, **kw)
     check(lib().vai_attention_launch(ctypes.byref(a), stream), "vai_attention_launch")
+    check(lib().vai_stream_sync(stream), "sync")   # the caller may drop its argument buffers on return
     return out
 
 

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
     const TileOrder order = TileOrder::make((M + BM - 1) / BM, GATED ? (p.H + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN, G);
     const uint32_t total = order.tiles_m * order.tiles_n;
     const int ktiles = (int)(K / BK);
-    const int my_tiles = (int)((total - blockIdx.x + G - 1) / G);
+    const int my_tiles = __builtin_amdgcn_readfirstlane((int)((total - blockIdx.x + G - 1) / G));
     const int S = my_tiles * ktiles;   // K stages this workgroup runs
 
     // Copies: waves 0-1 fill the A slab of a stage, waves 2-3 the B slab; copy
@@ -288,6 +288,12 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
             });
         }
         {
+            if (r + 1 == my_tiles) {
+                // the last tile's look-ahead copies and fragment reads have
+                // dead destinations: let them land before the epilogue
+                wait_vmcnt<0>();
+                wait_lgkmcnt0();
+            }
             uint32_t tm, tn;
             order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
             tile_store<GATED>(p, acc, cb, tm, tn, wm, wn, fr, fk);

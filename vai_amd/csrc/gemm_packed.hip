@@ -148,18 +148,19 @@ __device__ __forceinline__ void pk_col_bias(const GemmParams& p, uint32_t tn, in
 // row): buffer stores from a resource that starts at the tile's first row and
 // ends at the output's last row, so rows past M are dropped by the bounds
 // check; the common activations are compile-time (6 = the runtime kind).
-template <bool GATED, uint32_t EPI>
+template <bool GATED, uint32_t EPI, bool F16OUT = false>
 __device__ __forceinline__ void pk_store_fast(const GemmParams& p, float16v (&acc)[8][2], const float (&cb)[2],
                                               uint32_t tm, uint32_t tn, int w, int fr, int fk)
 {
     const uint32_t ld_out = GATED ? p.H : p.N;
     const uint32_t rows_left = p.M - tm * 256;
+    constexpr uint32_t ES = F16OUT ? 2 : 4;   // output element bytes
     const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((float*)p.C + (size_t)tm * 256 * ld_out), (short)0,
-        (int)std::min<size_t>((size_t)rows_left * ld_out * 4, 0x7FFFFFFF), 0x00020000);
+        (void*)((char*)p.C + (size_t)tm * 256 * ld_out * ES), (short)0,
+        (int)std::min<size_t>((size_t)rows_left * ld_out * ES, 0x7FFFFFFF), 0x00020000);
     const uint32_t col0 = GATED ? tn * 128 + w * 32 + fr : tn * 256 + w * 64 + fr;
-    const uint32_t lane_off = (4 * fk * ld_out + col0) * 4;
-    const uint32_t row_bytes = ld_out * 4;
+    const uint32_t lane_off = (4 * fk * ld_out + col0) * ES;
+    const uint32_t row_bytes = ld_out * ES;
     const uint32_t epi = p.epilogue;
     const float s = p.scalar_scale;
     constexpr int JN = GATED ? 1 : 2;
@@ -173,8 +174,11 @@ __device__ __forceinline__ void pk_store_fast(const GemmParams& p, float16v (&ac
                     v = act<EPI>(agpr_read(acc[i][0][rr]) + cb[0], epi) * (agpr_read(acc[i][1][rr]) + cb[1]);
                 else
                     v = s * act<EPI>(agpr_read(acc[i][j][rr]) + cb[j], epi);
-                const uint32_t voff = lane_off + (uint32_t)(i * 32 + (rr % 4) + 8 * (rr / 4)) * row_bytes + j * 128;
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out, (int)voff, 0, 0);
+                const uint32_t voff = lane_off + (uint32_t)(i * 32 + (rr % 4) + 8 * (rr / 4)) * row_bytes + j * 32 * ES;
+                if constexpr (F16OUT)
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (half_t)v), out, (int)voff, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out, (int)voff, 0, 0);
             });
             __builtin_amdgcn_sched_barrier(0);   // 16 outputs at a time: few live registers
         });
@@ -238,6 +242,12 @@ __device__ __forceinline__ void pk_store(const GemmParams& p, float16v (&acc)[8]
         case 3: pk_store_fast<GATED, 3>(p, acc, cb, tm, tn, w, fr, fk); break;   // GELU-tanh
         case 0: pk_store_fast<GATED, 0>(p, acc, cb, tm, tn, w, fr, fk); break;
         default: pk_store_fast<GATED, 6>(p, acc, cb, tm, tn, w, fr, fk); break;
+        }
+    } else if (cols_in && plain && p.c_dtype == DT_F16) {
+        switch (p.epilogue) {
+        case 4: pk_store_fast<GATED, 4, true>(p, acc, cb, tm, tn, w, fr, fk); break;   // SiLU
+        case 0: pk_store_fast<GATED, 0, true>(p, acc, cb, tm, tn, w, fr, fk); break;
+        default: pk_store_fast<GATED, 6, true>(p, acc, cb, tm, tn, w, fr, fk); break;
         }
     } else {
         pk_store_any<GATED>(p, acc, cb, tm, tn, w, fr, fk);
@@ -450,6 +460,14 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         here.kt = ktiles - 1;
         stage(g, here, next, has_next, acc, fb1, fb0);
         ++g;
+        if (!has_next) {
+            // The last unit's look-ahead loads (clamped copies, B fragments
+            // and A fragment reads of a stage that never runs) have dead
+            // destinations: let them land before the epilogue reuses
+            // registers, so no late return can overwrite a value being stored.
+            pk_wait_vmcnt<0>();
+            pk_wait_lgkmcnt0();
+        }
         pk_store<GATED>(up, acc, cb, here.tm, here.tn, wave, fr, fk);
     }
     pk_wait_vmcnt<0>();   // the clamped copies land before the workgroup retires

@@ -56,6 +56,14 @@ template <int BK, int STAGES> struct Cfg {
 };
 }
 
+// Keeps a substep's MFMA operands allocated until all of its MFMAs have
+// issued: the fragment reads interleaved with those MFMAs then cannot be
+// given a register an issued-but-not-started MFMA still has to read.
+__device__ __forceinline__ void keep_operands(const half8 (&a)[4], const half8 (&b)[4])
+{
+    asm volatile("" ::"v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+}
+
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt()
@@ -266,6 +274,7 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
                     }
                     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
                     __builtin_amdgcn_sched_barrier(0);   // substeps do not mix
+                    keep_operands(fa[cur], fb[cur]);
                 } else {
                     // Last substep: half its MFMAs cover the stage barrier; after it
                     // slot g is free for stage g + STAGES and stage g + 1 is read.
@@ -284,16 +293,11 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
                     }
                     __builtin_amdgcn_sched_barrier(0);
+                    keep_operands(fa[cur], fb[cur]);
                 }
             });
         }
         {
-            if (r + 1 == my_tiles) {
-                // the last tile's look-ahead copies and fragment reads have
-                // dead destinations: let them land before the epilogue
-                wait_vmcnt<0>();
-                wait_lgkmcnt0();
-            }
             uint32_t tm, tn;
             order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
             tile_store<GATED>(p, acc, cb, tm, tn, wm, wn, fr, fk);

@@ -104,6 +104,15 @@ hipError_t gemm_pack_weight(void* dst, const void* w, uint32_t N, uint32_t K, ui
     return hipGetLastError();
 }
 
+// Keeps a substep's MFMA operands allocated until all of its MFMAs have
+// issued: the fragment loads interleaved with those MFMAs then cannot be
+// given a register an issued-but-not-started MFMA still has to read.
+__device__ __forceinline__ void keep_operands(const half8 (&a)[8], const half8 (&b)[2])
+{
+    asm volatile("" ::"v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+                 "v"(b[0]), "v"(b[1]));
+}
+
 template <int N>
 __device__ __forceinline__ void pk_wait_vmcnt()
 {
@@ -233,6 +242,14 @@ __device__ __forceinline__ void pk_store(const GemmParams& p, float16v (&acc)[8]
                                          uint32_t tm, uint32_t tn, int w, int fr, int fk)
 {
     __builtin_amdgcn_sched_barrier(0);
+    // Every accumulator passes through an (empty) asm first, so no MFMA can
+    // be moved past this point into the epilogue's blocks; the s_nops then
+    // give the last MFMA its result-to-read distance (the agpr_read asm is
+    // opaque to the compiler's hazard checks).
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) asm volatile("" : "+a"(acc[i][j]));
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");   // MFMA result -> VALU read distance
     const bool cols_in = GATED ? tn * 128 + 128 <= p.H : tn * 256 + 256 <= p.N;
     const bool plain = GATED || (!p.residual && (!p.bias || p.bias_repeat == p.N));   // cb holds the bias
@@ -378,6 +395,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
                     if (u < 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load (B)
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                keep_operands(fa[c], cur[q]);
             } else {
                 load_b(b_at, nxt, q);
                 mfma_rows(acc, fa[c], cur[q], 0, 4);
@@ -401,6 +419,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                keep_operands(fa[c], cur[q]);
             }
         });
     };
@@ -460,14 +479,6 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         here.kt = ktiles - 1;
         stage(g, here, next, has_next, acc, fb1, fb0);
         ++g;
-        if (!has_next) {
-            // The last unit's look-ahead loads (clamped copies, B fragments
-            // and A fragment reads of a stage that never runs) have dead
-            // destinations: let them land before the epilogue reuses
-            // registers, so no late return can overwrite a value being stored.
-            pk_wait_vmcnt<0>();
-            pk_wait_lgkmcnt0();
-        }
         pk_store<GATED>(up, acc, cb, here.tm, here.tn, wave, fr, fk);
     }
     pk_wait_vmcnt<0>();   // the clamped copies land before the workgroup retires

@@ -183,6 +183,13 @@ __device__ __forceinline__ void tile_store(const GemmParams& p, float16v (&acc)[
                                            uint32_t tm, uint32_t tn, int wm, int wn, int fr, int fk)
 {
     __builtin_amdgcn_sched_barrier(0);
+    // Every accumulator passes through an (empty) asm first, so no MFMA can
+    // be moved past this point into the epilogue's blocks; the s_nops then
+    // give the last MFMA its result-to-read distance.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");   // MFMA result -> VALU read distance
     const bool cols_in = GATED ? tn * 128 + 128 <= p.H : tn * 256 + 256 <= p.N;
     const bool plain = GATED || (!p.residual && (!p.bias || p.bias_repeat == p.N));   // cb holds the bias

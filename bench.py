@@ -200,14 +200,18 @@ def build_cases(capi, stream, which):
         v = D(f16(rng.standard_normal((8, 1024, 256))))
         o = capi.DeviceArray((8, 1024, 256), np.float16)
         aa = capi.attention_args(o, q, k, v, scale=1.0 / 16, causal=True)
+        need = lib.vai_attention_workspace_size(ctypes.byref(aa))
+        wsa = capi.DeviceArray((max(need, 1),), np.uint8)
+        if need:
+            aa.workspace, aa.workspace_bytes = wsa.ptr, wsa.nbytes
         ra = ctypes.byref(aa)
 
         def fna(i):
             capi.check(lib.vai_attention_launch(ra, stream.ptr), "attention")
-        fna.keep = [q, k, v, o, aa]
+        fna.keep = [q, k, v, o, aa, wsa]
         flops = 4 * 8 * 256 * (1024 * 1025 // 2)   # QK^T and P.V over the visible (causal) pairs
         cases["attn"] = Case("attention Q,K,V[8,1024,256] fp16 causal, O = softmax(QK^T/16) V fp16 (fused)", "TFLOP/s",
-                             flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fna, "attention_fwd_kernel<256>", flops,
+                             flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fna, "attention_fwd_kernel<256> + attention_merge_kernel<256> (key range split in 256-key chunks)", flops,
                              4 * 8 * 1024 * 256 * 2, "f16", "attn")
 
     if "5" in which:   # YOLOX 3x3 conv, bias + SiLU

@@ -184,7 +184,9 @@ vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t
  * (causal, span). fp32 softmax statistics and accumulation; P is rounded to
  * fp16 for the P.V product. Q [batch,Hq,Tq,D], K/V [batch,Hkv,Tkv,D] fp16,
  * D in {64, 128, 256}; O [batch,Hq,Tq,D] in o_dtype (f32 or f16). A query
- * with no visible key gives zeros. Replaces the flash-attention dispatch of
+ * with no visible key gives zeros. Long key ranges may be split over
+ * workgroups and merged (then a workspace is needed). Replaces the
+ * flash-attention dispatch of
  * the reference's Attention node (/root/reference/vai/nodes/attention.h:
  * 979-1304, shaders/attention-fa.comp) for the no-cache case.
  * ------------------------------------------------------------------------- */
@@ -199,9 +201,15 @@ typedef struct {
     float scale;                  /* 0: 1/sqrt(head_dim), as attention.h:1254 */
     uint32_t causal;
     uint32_t span;
+    void* workspace;              /* vai_attention_workspace_size() bytes, or NULL when that is 0 */
+    size_t workspace_bytes;
 } vai_attention_args;
 
 vai_status vai_attention_launch(const vai_attention_args* args, vai_stream_t stream);
+/* Bytes of workspace a launch needs: nonzero when the query tiles alone do
+ * not fill the GPU and long key ranges are split over workgroups (partial
+ * results merged by a second pass, the split-K of attention-fa-reduce.comp). */
+size_t vai_attention_workspace_size(const vai_attention_args* args);
 
 /* ---------------------------------------------------------------------------
  * Device memory and streams: what the host side (vai::Tensor's pooled

@@ -22,6 +22,8 @@ pytestmark = pytest.mark.gpu
     (1, 2, 1, 257, 257, 64, True, 50, np.float32),       # sliding window
     (2, 2, 2, 100, 130, 128, False, 0, np.float32),      # no mask, batch 2
     (1, 1, 1, 70, 40, 64, True, 0, np.float32),          # Tq > Tkv: the first 30 queries see no key
+    (1, 2, 2, 64, 1000, 128, False, 0, np.float32),      # one query tile, 16 key tiles: split in 4 and merged
+    (1, 2, 2, 600, 520, 64, True, 0, np.float16),        # split, and a query tile that sees no key
 ])
 def test_attention(gpu, b, hq, hkv, tq, tkv, d, causal, span, odt):
     rng = np.random.default_rng(7)
@@ -48,3 +50,19 @@ def test_attention_rejects(gpu):
     a = gpu.attention_args(D((1, 1, 8, 96), np.float32), D((1, 1, 8, 96), np.float16), D((1, 1, 8, 96), np.float16),
                            D((1, 1, 8, 96), np.float16))
     assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1005
+
+
+def test_attention_workspace(gpu):
+    """The key-range split asks for a workspace (config 4's shape: 128 query
+    tiles leave CUs idle) and refuses to run without one; a shape whose query
+    tiles fill the GPU needs none."""
+    import ctypes
+    D = gpu.DeviceArray
+    q = D((8, 1024, 256), np.float16)
+    a = gpu.attention_args(D((8, 1024, 256), np.float32), q, q, q, causal=True)
+    need = gpu.lib().vai_attention_workspace_size(ctypes.byref(a))
+    assert need > 0
+    assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1004
+    q2 = D((32, 1024, 64), np.float16)
+    a2 = gpu.attention_args(D((32, 1024, 64), np.float32), q2, q2, q2, causal=True)
+    assert gpu.lib().vai_attention_workspace_size(ctypes.byref(a2)) == 0

@@ -21,7 +21,7 @@ EXPORTS = [
     "vai_linear_launch", "vai_linear_workspace_size", "vai_linear_plan", "vai_gated_mul_launch",
     "vai_linear_packed_weight_size", "vai_linear_pack_weight",
     "vai_conv2d_launch", "vai_conv2d_workspace_size", "vai_conv2d_packed_weight_size", "vai_conv2d_pack_weight",
-    "vai_attn_scores_launch", "vai_attention_launch",
+    "vai_attn_scores_launch", "vai_attention_launch", "vai_attention_workspace_size",
     "vai_device_count", "vai_set_device", "vai_malloc", "vai_free", "vai_memcpy_h2d", "vai_memcpy_d2h",
     "vai_memcpy_d2d", "vai_memset", "vai_stream_create", "vai_stream_destroy", "vai_stream_sync",
     "vai_device_sync", "vai_status_string", "vai_event_create", "vai_event_destroy", "vai_event_record",
@@ -76,6 +76,7 @@ class AttentionArgs(ctypes.Structure):
         ("batch", ctypes.c_uint32), ("hq", ctypes.c_uint32), ("hkv", ctypes.c_uint32),
         ("tq", ctypes.c_uint32), ("tkv", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
         ("scale", ctypes.c_float), ("causal", ctypes.c_uint32), ("span", ctypes.c_uint32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -109,6 +110,8 @@ def lib():
         L.vai_conv2d_pack_weight.argtypes = [ctypes.POINTER(Conv2dArgs), vp, sz, vp]
         L.vai_attn_scores_launch.argtypes = [ctypes.POINTER(AttnScoresArgs), vp]
         L.vai_attention_launch.argtypes = [ctypes.POINTER(AttentionArgs), vp]
+        L.vai_attention_workspace_size.argtypes = [ctypes.POINTER(AttentionArgs)]
+        L.vai_attention_workspace_size.restype = sz
         L.vai_malloc.argtypes = [ctypes.POINTER(vp), sz]
         L.vai_free.argtypes = [vp]
         L.vai_memcpy_h2d.argtypes = [vp, vp, sz, vp]
@@ -361,6 +364,10 @@ def attention_args(out, q, k, v, *, scale=None, causal=True, span=0):
 
 def attention(out, q, k, v, stream=None, **kw):
     a = attention_args(out, q, k, v, **kw)
+    need = lib().vai_attention_workspace_size(ctypes.byref(a))
+    ws = DeviceArray((need,), np.uint8) if need else None
+    if ws is not None:
+        a.workspace, a.workspace_bytes = ws.ptr, ws.nbytes
     check(lib().vai_attention_launch(ctypes.byref(a), stream), "vai_attention_launch")
     check(lib().vai_stream_sync(stream), "sync")   # the caller may drop its argument buffers on return
     return out

@@ -41,6 +41,27 @@ template <int D> struct Lds {
 
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 
+// The 64-key tiles query tile qt can see: [tb, te).
+__host__ __device__ inline void fa_tile_range(const AttnParams& p, uint32_t qt, int64_t& tb, int64_t& te)
+{
+    const int64_t off = (int64_t)p.tkv - (int64_t)p.tq, q0 = (int64_t)qt * fa::BQ;
+    int64_t kend = (int64_t)p.tkv;
+    if (p.causal) kend = std::min<int64_t>(kend, q0 + fa::BQ - 1 + off + 1);
+    int64_t kbeg = 0;
+    if (p.span) kbeg = std::max<int64_t>(0, q0 + off + 1 - (int64_t)p.span);
+    tb = kbeg / fa::BKV;
+    te = kend <= kbeg ? tb : (kend + fa::BKV - 1) / fa::BKV;
+}
+
+// Chunks of query tile qt (at least one, so that every tile writes output).
+__host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt)
+{
+    int64_t tb, te;
+    fa_tile_range(p, qt, tb, te);
+    const int64_t n = te - tb;
+    return n <= 0 ? 1u : (uint32_t)((n + p.chunk_tiles - 1) / p.chunk_tiles);
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
 {
@@ -52,8 +73,26 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const uint32_t Tq = p.tq, Tkv = p.tkv;
-    // the longest causal walks (the last query tiles) start first
-    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * BQ, h = blockIdx.y, b = blockIdx.z;
+    const uint32_t h = blockIdx.y, b = blockIdx.z, nqt = (Tq + BQ - 1) / BQ;
+    // Work unit -> (query tile, key chunk). Units enumerate the query tiles
+    // from the last (the longest causal walks start first), chunk by chunk.
+    uint32_t qt, chunk = 0;
+    if (p.units == 0) {
+        qt = nqt - 1 - blockIdx.x;
+    } else {
+        uint32_t u = blockIdx.x;
+        qt = nqt - 1;
+        for (;;) {
+            const uint32_t nc = fa_chunks(p, qt);
+            if (u < nc || qt == 0) break;
+            u -= nc;
+            --qt;
+        }
+        chunk = u;
+        qt = __builtin_amdgcn_readfirstlane(qt);
+        chunk = __builtin_amdgcn_readfirstlane(chunk);
+    }
+    const uint32_t q0 = qt * BQ;
     const uint32_t hk = h / (p.hq / p.hkv);
     const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
     const half_t* K = (const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D;
@@ -67,12 +106,15 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
     for (int s = 0; s < KS; ++s)
         qf[s] = qrow < Tq ? *(const half8*)(Q + (size_t)qrow * D + s * 32 + lg * 8) : (half8)0;
 
-    // visible key range of the whole tile
-    int64_t kend = (int64_t)Tkv;
-    if (p.causal) kend = std::min<int64_t>(kend, (int64_t)q0 + BQ - 1 + off + 1);
-    int64_t kbeg = 0;
-    if (p.span) kbeg = std::max<int64_t>(0, (int64_t)q0 + off + 1 - (int64_t)p.span);
-    kbeg = kbeg / BKV * BKV;
+    // visible key tiles of the query tile, then this unit's chunk of them
+    int64_t tb, te;
+    fa_tile_range(p, qt, tb, te);
+    if (p.units != 0) {
+        const int64_t c0 = tb + (int64_t)chunk * p.chunk_tiles;
+        te = std::min<int64_t>(te, c0 + p.chunk_tiles);
+        tb = c0;
+    }
+    const int64_t kbeg = tb * BKV, kend = std::min<int64_t>(te * BKV, (int64_t)Tkv);
 
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
     const int64_t qpos = (int64_t)qrow + off;
@@ -184,6 +226,21 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
             }
     }
 
+    if (p.units != 0) {
+        // partial result: O unnormalised, (m, l) per row
+        const size_t gid = ((size_t)b * p.hq + h) * p.units + blockIdx.x;
+        float* wo = p.ws_o + gid * BQ * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int d = 0; d < DB; ++d) wo[(size_t)(wave * 16 + 4 * lg + r) * D + d * 16 + lr] = o[d][r];
+        if (lg == 0) {
+            float* wml = p.ws_ml + (gid * BQ + wave * 16 + lr) * 2;
+            wml[0] = m;
+            wml[1] = l;
+        }
+        return;
+    }
     // O / l per row, then the store: lane holds rows 4lg + r, column d*16 + lr
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
@@ -195,6 +252,65 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
 #pragma unroll
         for (int d = 0; d < DB; ++d) st(p.out, p.o_dtype, base + d * 16, o[d][r] * ir);
     }
+}
+
+// Merge of the key chunks of one query tile: O = sum_c 2^(m_c - M) O_c /
+// sum_c 2^(m_c - M) l_c, M = max_c m_c (m in log2 units); 0 without keys.
+template <int D>
+__global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
+{
+    using namespace fa;
+    constexpr int MAXC = 64, RG = 8;   // chunks per query tile; rows per workgroup
+    __shared__ float wgt[RG][MAXC];
+    const uint32_t nqt = (p.tq + BQ - 1) / BQ, qt = blockIdx.x / (BQ / RG), r0 = (blockIdx.x % (BQ / RG)) * RG;
+    const uint32_t h = blockIdx.y, b = blockIdx.z;
+    uint32_t u0 = 0;
+    for (uint32_t q = nqt - 1; q > qt; --q) u0 += fa_chunks(p, q);
+    const uint32_t nc = fa_chunks(p, qt);
+    const size_t g0 = ((size_t)b * p.hq + h) * p.units + u0;
+    // per-row chunk weights 2^(m_c - M) / sum_c 2^(m_c - M) l_c
+    if (threadIdx.x < RG) {
+        const uint32_t row = r0 + threadIdx.x;
+        float M = -__builtin_inff();
+        for (uint32_t c = 0; c < nc; ++c) M = fmaxf(M, p.ws_ml[((g0 + c) * BQ + row) * 2]);
+        float den = 0.f;
+        for (uint32_t c = 0; c < nc; ++c) {
+            const float* ml = p.ws_ml + ((g0 + c) * BQ + row) * 2;
+            const float w = (M == -__builtin_inff() || ml[0] == -__builtin_inff()) ? 0.f
+                                                                                   : __builtin_amdgcn_exp2f(ml[0] - M);
+            wgt[threadIdx.x][c] = w;
+            den += w * ml[1];
+        }
+        const float inv = den > 0.f ? 1.0f / den : 0.f;
+        for (uint32_t c = 0; c < nc; ++c) wgt[threadIdx.x][c] *= inv;
+    }
+    __syncthreads();
+    // thread t: rows r0 + (t*4 / D) .., 4 consecutive columns (16-byte loads)
+    for (uint32_t e = threadIdx.x * 4; e < RG * D; e += 256 * 4) {
+        const uint32_t rl = e / D, col = e % D, qrow = qt * BQ + r0 + rl;
+        if (qrow >= p.tq) continue;
+        float4v acc = (float4v)0.f;
+        for (uint32_t c = 0; c < nc; ++c)
+            acc += wgt[rl][c] * *(const float4v*)(p.ws_o + ((g0 + c) * BQ + r0 + rl) * D + col);
+        const size_t o = (((size_t)b * p.hq + h) * p.tq + qrow) * D + col;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) st(p.out, p.o_dtype, o + k, acc[k]);
+    }
+}
+
+uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles)
+{
+    AttnParams q = p;
+    q.chunk_tiles = chunk_tiles;
+    const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
+    uint32_t units = 0;
+    for (uint32_t qt = 0; qt < nqt; ++qt) units += fa_chunks(q, qt);
+    return units == nqt ? 0u : units;
+}
+
+size_t attention_workspace_bytes(const AttnParams& p, uint32_t units)
+{
+    return (size_t)p.batch * p.hq * units * fa::BQ * (p.head_dim + 2) * sizeof(float);
 }
 
 bool attention_ok(const AttnParams& p)
@@ -214,8 +330,13 @@ static hipError_t attention_launch_d(const AttnParams& p, hipStream_t s)
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid((p.tq + fa::BQ - 1) / fa::BQ, p.hq, p.batch);
+    const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
+    const dim3 grid(p.units ? p.units : nqt, p.hq, p.batch);
     hipLaunchKernelGGL(attention_fwd_kernel<D>, grid, dim3(256), fa::Lds<D>::BYTES, s, p);
+    if (p.units == 0) return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_merge_kernel<D>, dim3(nqt * (fa::BQ / 8), p.hq, p.batch), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -290,18 +290,47 @@ vai_status vai_linear_pack_weight(const vai_linear_args* a, void* packed, size_t
                                        (hipStream_t)stream));
 }
 
-vai_status vai_attention_launch(const vai_attention_args* a, vai_stream_t stream)
+static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
 {
-    if (!a || !a->out || !a->q || !a->k || !a->v) return VAI_ERR_INVALID_ARG;
+    if (!a || !a->q || !a->k || !a->v) return VAI_ERR_INVALID_ARG;
     if (a->i_dtype != VAI_DTYPE_F16 || !dtype_ok(a->o_dtype)) return VAI_ERR_DTYPE;
     if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || a->tkv == 0 || a->hq % a->hkv != 0)
         return VAI_ERR_SHAPE;
-    AttnParams p{};
+    p = AttnParams{};
     p.out = a->out; p.q = a->q; p.k = a->k; p.v = a->v; p.o_dtype = a->o_dtype;
     p.batch = a->batch; p.hq = a->hq; p.hkv = a->hkv; p.tq = a->tq; p.tkv = a->tkv; p.head_dim = a->head_dim;
     p.scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)a->head_dim);
     p.causal = a->causal; p.span = a->span;
     if (!attention_ok(p)) return VAI_ERR_UNSUPPORTED;
+    // Split the key ranges (chunks of 4 tiles = 256 keys) only when the query
+    // tiles alone leave CUs idle.
+    const uint32_t tiles = a->batch * a->hq * ((a->tq + 63) / 64);
+    // at most 64 chunks per query tile (the merge holds their weights in LDS)
+    const uint32_t key_tiles = (a->tkv + 63) / 64;
+    p.chunk_tiles = std::max<uint32_t>(4, (key_tiles + 63) / 64);
+    p.units = tiles < kCUs ? attention_units(p, p.chunk_tiles) : 0;
+    return VAI_OK;
+}
+
+size_t vai_attention_workspace_size(const vai_attention_args* a)
+{
+    AttnParams p;
+    if (attention_params(a, p) != VAI_OK || p.units == 0) return 0;
+    return attention_workspace_bytes(p, p.units);
+}
+
+vai_status vai_attention_launch(const vai_attention_args* a, vai_stream_t stream)
+{
+    AttnParams p;
+    if (a && !a->out) return VAI_ERR_INVALID_ARG;
+    vai_status st = attention_params(a, p);
+    if (st != VAI_OK) return st;
+    if (p.units) {
+        const size_t need = attention_workspace_bytes(p, p.units);
+        if (!a->workspace || a->workspace_bytes < need) return VAI_ERR_WORKSPACE;
+        p.ws_o = (float*)a->workspace;
+        p.ws_ml = p.ws_o + (size_t)a->batch * a->hq * p.units * 64 * a->head_dim;
+    }
     return hip_status(attention_launch(p, (hipStream_t)stream));
 }
 

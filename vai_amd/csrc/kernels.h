@@ -106,8 +106,19 @@ struct AttnParams {
     uint32_t batch, hq, hkv, tq, tkv, head_dim;
     float scale;
     uint32_t causal, span;
+    // Key-range split (0 units: each workgroup walks all of its keys and
+    // writes O). Otherwise each query tile's keys are cut into chunks of
+    // chunk_tiles 64-key tiles, `units` work units per head; partial O and
+    // (max, sum) go to ws_o / ws_ml and a merge pass combines them.
+    uint32_t units, chunk_tiles;
+    float* ws_o;                  // [batch*hq*units][64][head_dim]
+    float* ws_ml;                 // [batch*hq*units][64][2]
 };
 bool attention_ok(const AttnParams& p);
+// Units per head for p's shape (0 when no query tile needs splitting), and
+// the workspace the split needs.
+uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles);
+size_t attention_workspace_bytes(const AttnParams& p, uint32_t units);
 hipError_t attention_launch(const AttnParams& p, hipStream_t s);
 
 // Implicit-GEMM convolution, fp16 weights packed per tap in MFMA fragment order.

@@ -118,6 +118,20 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
 
     for (uint32_t kb = 0; kb < K; kb += KB) {
+        // 0. Few input rows: this lane's X chunks (L2-resident) first, so that
+        //    loads return in order X, then W chunk by chunk, and each chunk's
+        //    products start as soon as that chunk lands.
+        typedef TI xvec __attribute__((ext_vector_type(EPC)));
+        xvec xr[MP <= 2 ? KCH : 1][MP <= 2 ? MP : 1];
+        if constexpr (MP <= 2) {
+#pragma unroll
+            for (int c = 0; c < KCH; ++c) {
+                const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
+#pragma unroll
+                for (int m = 0; m < MP; ++m)
+                    xr[c][m] = ((uint32_t)m < M && k < K) ? *(const xvec*)(X + (size_t)m * K + k) : (xvec)0;
+            }
+        }
         // 1. Every W load of this block for this wave's R rows, issued up front.
         wvec wv[R][KCH];
 #pragma unroll
@@ -131,15 +145,13 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
                     wv[r][c] = (wvec)0;
             }
         if constexpr (MP <= 2) {
-            // 2'. Few input rows: each lane loads its own X chunks (L2-resident)
-            //     straight into registers; no LDS, no barrier.
+            // 2'. Few input rows: the X chunks loaded in step 0, in registers;
+            //     no LDS, no barrier.
 #pragma unroll
             for (int c = 0; c < KCH; ++c) {
-                const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
 #pragma unroll
                 for (int m = 0; m < MP; ++m) {
-                    typedef TI xvec __attribute__((ext_vector_type(EPC)));
-                    const xvec xv = ((uint32_t)m < M && k < K) ? *(const xvec*)(X + (size_t)m * K + k) : (xvec)0;
+                    const xvec xv = xr[c][m];
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         float s = acc[m * R + r];

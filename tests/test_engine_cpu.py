@@ -60,6 +60,7 @@ def test_only_output_to_input_connections(pv):
     (lambda pv: pv.nodes.ConvolutionNode(in_channels=3, out_channels=4, kernel_size=3, stride=0), "stride"),
     (lambda pv: pv.nodes.LinearNode(in_dim=0, out_dim=3), "positive"),
     (lambda pv: pv.nodes.AttentionScoresNode(num_q_heads=3, head_dim=8, num_kv_heads=2), "multiple"),
+    (lambda pv: pv.nodes.AttentionNode(num_q_heads=3, head_dim=8, num_kv_heads=2), "multiple"),
 ])
 def test_config_checks(pv, make, msg):
     class Net(pv.NeuralNet):

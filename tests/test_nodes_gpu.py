@@ -157,6 +157,24 @@ def test_attention_scores_node(gpu, hq, hkv, tq, tkv, d, causal):
     assert_close(got, oracle.attn_scores(q, k, causal=causal), FP32)
 
 
+@pytest.mark.parametrize("hq, hkv, tq, tkv, d, causal, span", [(4, 2, 100, 100, 128, True, 0),
+                                                               (2, 2, 64, 1000, 64, False, 0),
+                                                               (2, 1, 257, 257, 64, True, 50)])
+def test_attention_node(gpu, hq, hkv, tq, tkv, d, causal, span):
+    """The engine's Attention node (Q, K, V -> out0) runs the fused kernel,
+    binding its key-split partials to the "partialO" temporary when the
+    launch splits key ranges (the 1000-key case)."""
+    pv = pyvai()
+    rng = np.random.default_rng(3)
+    q = draw((1, hq, tq, d), rng, np.float16)
+    k = draw((1, hkv, tkv, d), rng, np.float16)
+    v = draw((1, hkv, tkv, d), rng, np.float16)
+    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d, num_kv_heads=hkv, causal=causal,
+                                                   span=span), ["Q", "K", "V"], {})
+    got = forward(net, {"Q": q, "K": k, "V": v}).astype(np.float32)
+    assert_close(got, oracle.attention(q, k, v, causal=causal, span=span, out_dtype=np.float32), FP16)
+
+
 def test_gpt2_cfc_through_the_engine(gpu):
     """BASELINE config 1 via input - linear - output."""
     import os, sys

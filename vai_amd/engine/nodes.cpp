@@ -335,4 +335,77 @@ void AttentionScores::run(CommandStream& cmd)
     check(vai_attn_scores_launch(&a, (vai_stream_t)cmd.stream()), "AttentionScores");
 }
 
+// ------------------------------------------------------------- Attention ----
+
+Attention::Attention(Config config) : config_(config)
+{
+    if (config_.numKVHeads == 0) config_.numKVHeads = config_.numQHeads;
+    require(config_.numQHeads > 0 && config_.headDim > 0, "Attention: heads and headDim must be positive");
+    require(config_.numQHeads % config_.numKVHeads == 0, "Attention: numQHeads must be a multiple of numKVHeads");
+    addSlot("out0", NodeSlot::output);
+    addSlot("Q", NodeSlot::input);
+    addSlot("K", NodeSlot::input);
+    addSlot("V", NodeSlot::input);
+    addSlot("partialO", NodeSlot::temporary);
+}
+
+vai_attention_args Attention::args(bool withBuffers) const
+{
+    vai_attention_args a{};
+    a.o_dtype = code(outputDtype());
+    a.i_dtype = code((*this)["Q"].dtype());
+    a.batch = batch_;
+    a.hq = config_.numQHeads;
+    a.hkv = config_.numKVHeads;
+    a.tq = tq_;
+    a.tkv = tkv_;
+    a.head_dim = config_.headDim;
+    a.scale = config_.scale;
+    a.causal = config_.causal ? 1 : 0;
+    a.span = config_.span;
+    // the size query needs non-null operands; their values do not matter
+    alignas(16) static char dummy[16];
+    a.q = a.k = a.v = dummy;
+    a.out = dummy;
+    if (withBuffers) {
+        a.out = (*this)["out0"].devicePtr();
+        a.q = (*this)["Q"].devicePtr();
+        a.k = (*this)["K"].devicePtr();
+        a.v = (*this)["V"].devicePtr();
+        const Tensor& part = (*this)["partialO"];
+        a.workspace = part.validShape() ? part.devicePtr() : nullptr;
+        a.workspace_bytes = part.validShape() ? part.numBytes() : 0;
+    }
+    return a;
+}
+
+void Attention::prepare()
+{
+    const Tensor& q = (*this)["Q"];
+    const Tensor& k = (*this)["K"];
+    const Tensor& v = (*this)["V"];
+    const auto& qs = q.shape();
+    const auto& ks = k.shape();
+    require(qs.size() >= 3 && ks.size() == qs.size() && v.shape() == ks, "Attention: Q, K, V must be [..., H, T, D]");
+    require(qs.back() == config_.headDim && ks.back() == config_.headDim, "Attention: headDim mismatch");
+    require(qs[qs.size() - 3] == config_.numQHeads && ks[ks.size() - 3] == config_.numKVHeads,
+            "Attention: head counts mismatch");
+    require(q.dtype() == Dtype::Fp16 && k.dtype() == Dtype::Fp16 && v.dtype() == Dtype::Fp16,
+            "Attention: Q, K and V must be fp16");
+    batch_ = outerSize(qs, 3);
+    require(outerSize(ks, 3) == batch_, "Attention: Q and K batch axes differ");
+    tq_ = qs[qs.size() - 2];
+    tkv_ = ks[ks.size() - 2];
+    (*this)["out0"] = Tensor(qs, outputDtype());
+    const vai_attention_args a = args(false);
+    const size_t ws = vai_attention_workspace_size(&a);
+    (*this)["partialO"] = ws ? Tensor({uint32_t((ws + 3) / 4)}, Dtype::Fp32) : Tensor();
+}
+
+void Attention::run(CommandStream& cmd)
+{
+    const vai_attention_args a = args(true);
+    check(vai_attention_launch(&a, (vai_stream_t)cmd.stream()), "Attention");
+}
+
 }   // namespace vai::node

@@ -146,5 +146,33 @@ private:
     uint32_t batch_ = 1, tq_ = 0, tkv_ = 0;
 };
 
+// The reference's Attention node without a KV cache (/root/reference/vai/
+// nodes/attention.h:216-240, 979-1304): out0 = softmax(scale * Q K^T + mask) V
+// per head, Q [..., numQHeads, Tq, headDim], K / V [..., numKVHeads, Tkv,
+// headDim] fp16, out0 like Q in the node's output dtype. The mask is the
+// causal / sliding-window rule (the reference reads it from setCausalMask's
+// buffer). "partialO" holds the key-split partials when a launch uses them.
+class Attention : public Node
+{
+public:
+    struct Config {
+        uint32_t headDim;
+        uint32_t numQHeads;
+        uint32_t numKVHeads = 0;   // 0: numQHeads (no GQA)
+        bool causal = true;
+        uint32_t span = 0;         // sliding window; 0: none
+        float scale = 0.0f;        // 0: 1/sqrt(headDim), as attention.h:1254
+    } config_;
+
+    explicit Attention(Config config);
+    void prepare() override;
+    void run(CommandStream& cmd) override;
+    const char* kind() const override { return "Attention"; }
+
+private:
+    vai_attention_args args(bool withBuffers) const;
+    uint32_t batch_ = 1, tq_ = 0, tkv_ = 0;
+};
+
 }   // namespace node
 }   // namespace vai

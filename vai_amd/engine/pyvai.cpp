@@ -195,4 +195,13 @@ PYBIND11_MODULE(_pyvai, m)
              }),
              py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0, py::arg("causal") = true,
              py::arg("span") = 0, py::arg("scale") = 0.0f);
+    py::class_<node::Attention, Node>(nodes, "AttentionNode")
+        .def(py::init([](uint32_t num_q_heads, uint32_t head_dim, uint32_t num_kv_heads, bool causal, uint32_t span,
+                         float scale) {
+                 node::Attention::Config c{.headDim = head_dim, .numQHeads = num_q_heads, .numKVHeads = num_kv_heads,
+                                           .causal = causal, .span = span, .scale = scale};
+                 return std::make_unique<node::Attention>(c);
+             }),
+             py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0, py::arg("causal") = true,
+             py::arg("span") = 0, py::arg("scale") = 0.0f);
 }

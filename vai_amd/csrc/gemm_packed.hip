@@ -384,7 +384,10 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
         static_for<4>([&](auto Q) __attribute__((always_inline)) {
             constexpr int q = Q, c = q & 1, n = c ^ 1;
             if constexpr (q < 3) {
+                // substep 2 also loads substep 3's B, so that every B load of
+                // the stage is a substep old at the stage-end wait
                 load_b(b_at, nxt, q);
+                if constexpr (q == 2) load_b(b_at, nxt, 3);
                 read_a(g, q + 1, fa[n]);
                 mfma_rows(acc, fa[c], cur[q], 0, 8);
 #pragma unroll
@@ -392,22 +395,20 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read (A)
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (u < 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load (B)
+                    if (u < (q == 2 ? 4 : 2)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load (B)
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 keep_operands(fa[c], cur[q]);
             } else {
-                load_b(b_at, nxt, q);
                 mfma_rows(acc, fa[c], cur[q], 0, 4);
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                }
                 __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
                 __builtin_amdgcn_sched_barrier(0);
                 pk_wait_lgkmcnt0();                              // this wave's reads of slot g are done
-                pk_wait_vmcnt<A_LOADS + 2 * B_LOADS>();          // A(g+1) landed: B(g), A(g+2), B(g+1) may not
+                // A(g+1) landed. Only the A(g+2) copies may still be in
+                // flight: the count relies on the LDS copies completing in
+                // order among themselves, never on their order relative to
+                // the B loads into VGPRs or the epilogue's stores.
+                pk_wait_vmcnt<A_LOADS>();
                 __builtin_amdgcn_s_barrier();
                 issue_a(g + SLOTS, ahead(here, next, has_next, SLOTS));
                 read_a(g + 1, 0, fa[n]);
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(256, 1) void gemm_packed_kernel(GemmParams p, const
 #pragma unroll
     for (int q = 0; q < 4; ++q) load_b(here, fb0, q);
     issue_a(2, Pos{here.tm, here.tn, 2, here.kb, here.split});
-    pk_wait_vmcnt<(SLOTS - 1) * A_LOADS + B_LOADS>();
+    pk_wait_vmcnt<(SLOTS - 1) * A_LOADS>();   // A(0) and B(0) landed; A(1), A(2) may not
     __builtin_amdgcn_s_barrier();
     read_a(0, 0, fa[0]);
 

@@ -58,8 +58,8 @@ __host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt)
 {
     int64_t tb, te;
     fa_tile_range(p, qt, tb, te);
-    const int64_t n = te - tb;
-    return n <= 0 ? 1u : (uint32_t)((n + p.chunk_tiles - 1) / p.chunk_tiles);
+    const int64_t n = te - tb;   // at most Tkv / 64: a 32-bit division suffices
+    return n <= 0 ? 1u : ((uint32_t)n + p.chunk_tiles - 1) / p.chunk_tiles;
 }
 
 template <int D>
@@ -261,28 +261,56 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
 {
     using namespace fa;
     constexpr int MAXC = 64, RG = 8;   // chunks per query tile; rows per workgroup
+    static_assert(RG * 32 == 256, "one 32-lane group per row");
     __shared__ float wgt[RG][MAXC];
     const uint32_t nqt = (p.tq + BQ - 1) / BQ, qt = blockIdx.x / (BQ / RG), r0 = (blockIdx.x % (BQ / RG)) * RG;
     const uint32_t h = blockIdx.y, b = blockIdx.z;
-    uint32_t u0 = 0;
-    for (uint32_t q = nqt - 1; q > qt; --q) u0 += fa_chunks(p, q);
+    // first unit of query tile qt: the chunks of the later tiles (units run
+    // from the last query tile down), summed across a 64-lane group
+    __shared__ uint32_t first_unit;
+    if (threadIdx.x < 64) {
+        uint32_t n = 0;
+        for (uint32_t q = qt + 1 + threadIdx.x; q < nqt; q += 64) n += fa_chunks(p, q);
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) n += __shfl_xor(n, s, 64);
+        if (threadIdx.x == 0) first_unit = n;
+    }
+    __syncthreads();
+    const uint32_t u0 = first_unit;
     const uint32_t nc = fa_chunks(p, qt);
     const size_t g0 = ((size_t)b * p.hq + h) * p.units + u0;
-    // per-row chunk weights 2^(m_c - M) / sum_c 2^(m_c - M) l_c
-    if (threadIdx.x < RG) {
-        const uint32_t row = r0 + threadIdx.x;
-        float M = -__builtin_inff();
-        for (uint32_t c = 0; c < nc; ++c) M = fmaxf(M, p.ws_ml[((g0 + c) * BQ + row) * 2]);
-        float den = 0.f;
-        for (uint32_t c = 0; c < nc; ++c) {
-            const float* ml = p.ws_ml + ((g0 + c) * BQ + row) * 2;
-            const float w = (M == -__builtin_inff() || ml[0] == -__builtin_inff()) ? 0.f
-                                                                                   : __builtin_amdgcn_exp2f(ml[0] - M);
-            wgt[threadIdx.x][c] = w;
-            den += w * ml[1];
+    // per-row chunk weights 2^(m_c - M) / sum_c 2^(m_c - M) l_c: thread t
+    // takes row t / 32 and chunks t % 32, t % 32 + 32; max and sum reduce
+    // over the row's 32 lanes
+    {
+        const uint32_t rl = threadIdx.x / 32, c0 = threadIdx.x % 32, row = r0 + rl;
+        float mc[2], lc[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t c = c0 + 32 * k;
+            mc[k] = -__builtin_inff();
+            lc[k] = 0.f;
+            if (c < nc) {
+                const float2 ml = *(const float2*)(p.ws_ml + ((g0 + c) * BQ + row) * 2);
+                mc[k] = ml.x;
+                lc[k] = ml.y;
+            }
         }
+        float M = fmaxf(mc[0], mc[1]);
+#pragma unroll
+        for (int s = 16; s >= 1; s >>= 1) M = fmaxf(M, __shfl_xor(M, s, 32));
+        float w[2], den = 0.f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            w[k] = (M == -__builtin_inff() || mc[k] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(mc[k] - M);
+            den += w[k] * lc[k];
+        }
+#pragma unroll
+        for (int s = 16; s >= 1; s >>= 1) den += __shfl_xor(den, s, 32);
         const float inv = den > 0.f ? 1.0f / den : 0.f;
-        for (uint32_t c = 0; c < nc; ++c) wgt[threadIdx.x][c] *= inv;
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            if (c0 + 32 * k < nc) wgt[rl][c0 + 32 * k] = w[k] * inv;
     }
     __syncthreads();
     // thread t: rows r0 + (t*4 / D) .., 4 consecutive columns (16-byte loads)

@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="1,2,3,4,5,ffn,attn,5/k1s1,5/k3s2")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU-baseline leg (all configs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--repeats", type=int, default=3)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="REPS",
@@ -276,26 +276,99 @@ def time_case(capi, stream, case, steps, warmup, repeats):
     return float(np.median(per_step))
 
 
-def cpu_baseline(budget_s):
-    """The oracle's fp32 GEMV (the linear-slab contract) on the host, timed
-    on a bounded sample of config 2 (M=1): repeated full GEMVs for ~budget_s,
-    rotating over 6 copies of W (6 x 64 MiB fp32) so that the host's last-level
-    cache cannot serve W between calls, as HBM serves it on the GPU."""
+def cpu_samples(keys):
+    """The CPU baseline's bounded sample of each configuration: key ->
+    (call(i), work per call in the GPU line's unit, unit, description). The
+    calls run the OpenMP restatement in oracle/cpu_baseline.c on the same
+    shapes and dtypes (fp16 operands stay fp16 in memory and are widened by
+    F16C); GEMV bytes are the bytes each call really reads and writes."""
     from oracle import oracle
     rng = np.random.default_rng(0)
-    w0 = f16(rng.standard_normal((8192, 2048)) * 0.02).astype(np.float32)
-    ws = [w0.copy() for _ in range(6)]
-    x = f16(rng.standard_normal((1, 2048))).astype(np.float32)
-    oracle.gemm_f32(x, ws[0])
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        oracle.gemm_f32(x, ws[n % len(ws)])
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    byts = 2048 * 8192 * 2 + 2048 * 2 + 8192 * 4
-    return {"value": round(byts / dt / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
-            "sample": f"oracle fp32 GEMV (vai_oracle.c orc_gemm_f32) on config 2 M=1, W widened to fp32; "
-                      f"{n} calls in {budget_s:.0f}s rotating 6 W copies, bytes counted as the fp16 problem's"}
+    out = {}
+    for key in keys:
+        if key == "1":
+            w = (rng.standard_normal((3072, 768)) * 0.02).astype(np.float32)
+            b = (rng.standard_normal(3072) * 0.02).astype(np.float32)
+            x = rng.standard_normal((128, 768)).astype(np.float32)
+            o = np.empty((128, 3072), np.float32)
+            out[key] = (lambda i, x=x, w=w, b=b, o=o: oracle.cpu_linear(x, w, b, epi="GELU_TANH", out=o),
+                        2 * 128 * 768 * 3072 / 1e12, "TFLOP/s", "full config 1 (fp32 blocked GEMM + bias + GELU-tanh)")
+        elif key.startswith("2/M="):
+            m = int(key[4:])
+            w0 = f16(rng.standard_normal((8192, 2048)) * 0.02)
+            ws = [w0.copy() for _ in range(max(2, ROTATE_BYTES // w0.nbytes))]
+            x = f16(rng.standard_normal((m, 2048)))
+            o = np.empty((m, 8192), np.float32)
+            byts = 2048 * 8192 * 2 + m * 2048 * 2 + m * 8192 * 4
+            out[key] = (lambda i, x=x, ws=ws, o=o: oracle.cpu_linear(x, ws[i % len(ws)], out=o), byts / 1e9, "GB/s",
+                        f"full config 2 M={m} (fp16 W read as fp16 via F16C), rotating {len(ws)} W copies "
+                        f"({len(ws) * w0.nbytes >> 20} MiB) past the host caches")
+        elif key in ("3", "ffn"):
+            rows = 128
+            wg = f16(rng.standard_normal((8192, 3072)) * 0.02)
+            wu = f16(rng.standard_normal((8192, 3072)) * 0.02)
+            w = np.ascontiguousarray(np.concatenate([wg, wu], 0))
+            x = f16(rng.standard_normal((rows, 3072)))
+            o = np.empty((rows, 8192), np.float32)
+            if key == "3":
+                out[key] = (lambda i, x=x, w=w, o=o: oracle.cpu_linear(x, w, gated=True, gate_epi="SILU", out=o),
+                            2 * rows * 3072 * 16384 / 1e12, "TFLOP/s",
+                            f"config 3 on {rows} of the 2048 rows of X against the full gate/up weight")
+            else:
+                w2 = f16(rng.standard_normal((3072, 8192)) * 0.02)
+                o2 = np.empty((rows, 3072), np.float32)
+
+                def ffn(i, x=x, w=w, w2=w2, o=o, o2=o2):
+                    oracle.cpu_linear(x, w, gated=True, gate_epi="SILU", out=o)
+                    oracle.cpu_linear(o, w2, out=o2)
+                out[key] = (ffn, (2 * rows * 3072 * 16384 + 2 * rows * 8192 * 3072) / 1e12, "TFLOP/s",
+                            f"the FFN block on {rows} of the 2048 rows (fp32 activations between the two GEMMs)")
+        elif key in ("4", "attn"):
+            q = f16(rng.standard_normal((8, 1024, 256)))
+            k = f16(rng.standard_normal((8, 1024, 256)))
+            if key == "4":
+                s = np.empty((8, 1024, 1024), np.float32)
+                out[key] = (lambda i, q=q, k=k, s=s: oracle.cpu_attn_scores(q, k, scale=1 / 16, causal=True, out=s),
+                            41943040 / 1e9, "GB/s", "full config 4 (bytes counted as the GPU line's: Q, K, S)")
+            else:
+                v = f16(rng.standard_normal((8, 1024, 256)))
+                o = np.empty((8, 1024, 256), np.float32)
+                out[key] = (lambda i, q=q, k=k, v=v, o=o: oracle.cpu_attention(q, k, v, scale=1 / 16, causal=True, out=o),
+                            4 * 8 * 256 * (1024 * 1025 // 2) / 1e12, "TFLOP/s",
+                            "full config-4 attention (blocked scores, fp32 softmax, P.V; causal pairs only)")
+        elif key.startswith("5"):
+            ci, co, ks, st, hw = {"5": (128, 128, 3, 1, 80), "5/k1s1": (256, 128, 1, 1, 40),
+                                  "5/k3s2": (128, 256, 3, 2, 80)}[key]
+            w = f16(rng.standard_normal((co, ci, ks, ks)) * 0.03)
+            b = f16(rng.standard_normal(co) * 0.02).astype(np.float32)
+            x = f16(rng.uniform(-1, 1, (ci, hw, hw)))
+            ho = (hw - 1) // st + 1
+            o = np.empty((co, ho, ho), np.float32)
+            out[key] = (lambda i, x=x, w=w, b=b, st=st, o=o: oracle.cpu_conv2d(x, w, b, stride=st, epi="SILU", out=o),
+                        2 * ho * ho * co * ci * ks * ks / 1e12, "TFLOP/s",
+                        f"full {ks}x{ks}/s{st} conv (implicit GEMM per output row, K order c*k*k + kh*k + kw)")
+    return out
+
+
+def cpu_baseline(keys, budget_s):
+    """Each sample above run repeatedly for its share of budget_s (at least
+    one call) on the host cores, after one untimed call."""
+    from oracle import oracle
+    samples = cpu_samples(keys)
+    share = budget_s / max(1, len(samples))
+    res = {}
+    for key, (call, work, unit, desc) in samples.items():
+        call(0)
+        n, t0 = 0, time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < share:
+            call(n + 1)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res[key] = {"value": round(work / dt, 4 if unit == "TFLOP/s" else 3), "unit": unit,
+                    "cores": oracle.num_threads(), "kind": "port",
+                    "sample": f"oracle/cpu_baseline.c, {desc}; {n} calls in {dt * n:.1f} s"}
+        print(f"# cpu {key}: {res[key]['value']} {unit} ({n} calls)", file=sys.stderr, flush=True)
+    return res
 
 
 def traffic_probe(capi, stream, cases, reps):
@@ -344,6 +417,9 @@ def main():
         }
         print(f"# cfg {key}: {case.name}: {ms*1e3:.2f} us/step, {rate:.1f} {case.unit}, "
               f"{100*achieved/case.peak:.1f}% of {case.bound} peak [{case.kernel}]", file=sys.stderr, flush=True)
+    if not args.no_cpu:
+        for key, cb in cpu_baseline(list(report), args.cpu_seconds).items():
+            report[key]["cpu_baseline"] = cb
     prim = report.get("2/M=1") or next(iter(report.values()))
     line = {
         "metric": METRIC, "value": prim["value"], "unit": prim["unit"], "n_gpus": 1, "steps": args.steps,
@@ -351,7 +427,7 @@ def main():
         "vs_baseline": None, "dtype": prim["dtype"], "data": "synthetic",
         "config": {"workload": prim["workload"], "kernel": prim["kernel"]},
         "roofline": prim["roofline"],
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
+        "cpu_baseline": prim.get("cpu_baseline"),
         "configs": report,
     }
     print(json.dumps(line), flush=True)

@@ -4,8 +4,8 @@
  * Plain pointers and sizes only. Every buffer is device memory the caller owns
  * (hipMalloc'd, or any device-visible pointer); every launch is asynchronous on
  * the given stream and returns a vai_status (0 = success). Nothing throws
- * across this boundary. The library keeps no per-call state besides an
- * immutable kernel table.
+ * across this boundary. The library keeps no per-call state: besides its
+ * kernels it holds only per-device launch settings made once (thread-safe).
  *
  * Callers: the C++ nodes in vai_amd/engine (Linear::run, Convolution::run,
  * AttentionScores::run, GatedMul::run), which replace the reference's

@@ -186,5 +186,66 @@ def attention(q, k, v, *, scale=None, causal=True, span=0, out_dtype=np.float32)
     return O.astype(out_dtype)
 
 
+# ---- CPU baseline (cpu_baseline.c): the timed CPU restatement bench.py reports ----
+
+def _f32_or_none(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def cpu_linear(x, w, bias=None, *, epi="NONE", gated=False, gate_epi="SILU", out=None):
+    """fp32 O = epi(x w^T + b) (gated: gate_epi(g) * u over W = [gate; up]),
+    x and w fp32 or fp16; M <= 8 takes the streaming GEMV."""
+    x, w, bias = _c(x), _c(w), _f32_or_none(bias)
+    K, N = w.shape[-1], w.shape[0]
+    M = x.size // K
+    if out is None:
+        out = np.empty((M, N // 2 if gated else N), np.float32)
+    lib().cpb_linear(_p(out), _p(x), _dt(x), _p(w), _dt(w), _p(bias), ctypes.c_uint32(M), ctypes.c_uint32(N),
+                     ctypes.c_uint32(K), ctypes.c_int(EPILOGUES[epi]), ctypes.c_int(1 if gated else 0),
+                     ctypes.c_int(EPILOGUES[gate_epi]))
+    return out
+
+
+def cpu_conv2d(x, w, bias=None, *, stride=1, epi="NONE", out=None):
+    """One image x [Ci,Hi,Wi] (or [1,Ci,Hi,Wi]), w [Co,Ci,k,k]: fp32 same-padded conv."""
+    x, w, bias = _c(x), _c(w), _f32_or_none(bias)
+    Co, Ci, ks, _ = w.shape
+    Hi, Wi = x.shape[-2:]
+    assert x.size == Ci * Hi * Wi
+    Ho, Wo = (Hi - 1) // stride + 1, (Wi - 1) // stride + 1
+    if out is None:
+        out = np.empty((Co, Ho, Wo), np.float32)
+    lib().cpb_conv2d(_p(out), _p(x), _dt(x), _p(w), _dt(w), _p(bias), ctypes.c_uint32(Ci), ctypes.c_uint32(Hi),
+                     ctypes.c_uint32(Wi), ctypes.c_uint32(Co), ctypes.c_uint32(ks), ctypes.c_uint32(stride),
+                     ctypes.c_int(EPILOGUES[epi]))
+    return out
+
+
+def cpu_attn_scores(q, k, *, scale, causal=True, out=None):
+    """fp16 q [H,Tq,D], k [H,Tkv,D] -> fp32 S [H,Tq,Tkv], -inf where hidden."""
+    q, k = _c(q), _c(k)
+    assert q.dtype == np.float16 and k.dtype == np.float16
+    H, Tq, D = q.shape
+    Tkv = k.shape[1]
+    if out is None:
+        out = np.empty((H, Tq, Tkv), np.float32)
+    lib().cpb_attn_scores(_p(out), _p(q), _p(k), ctypes.c_uint32(H), ctypes.c_uint32(Tq), ctypes.c_uint32(Tkv),
+                          ctypes.c_uint32(D), ctypes.c_float(scale), ctypes.c_int(1 if causal else 0))
+    return out
+
+
+def cpu_attention(q, k, v, *, scale, causal=True, out=None):
+    """fp16 q [H,Tq,D], k and v [H,Tkv,D] -> fp32 softmax(scale q k^T + mask) v."""
+    q, k, v = _c(q), _c(k), _c(v)
+    assert q.dtype == k.dtype == v.dtype == np.float16
+    H, Tq, D = q.shape
+    Tkv = k.shape[1]
+    if out is None:
+        out = np.empty((H, Tq, D), np.float32)
+    lib().cpb_attention(_p(out), _p(q), _p(k), _p(v), ctypes.c_uint32(H), ctypes.c_uint32(Tq), ctypes.c_uint32(Tkv),
+                        ctypes.c_uint32(D), ctypes.c_float(scale), ctypes.c_int(1 if causal else 0))
+    return out
+
+
 def num_threads():
     return lib().orc_num_threads()

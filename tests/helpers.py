@@ -44,6 +44,23 @@ def max_rel_err(got, want):
     return float((np.abs(got[fin] - want[fin]) / np.maximum(np.abs(want[fin]), floor)).max())
 
 
+def cond_rel_err(got, want, mag):
+    """BASELINE's relative error with each element's floor raised to the
+    magnitude its fp32 accumulation works at: max |got-ref| / max(|ref|, mag),
+    mag = sum_k |a_k b_k| (carried through the epilogue). Any fp32-accumulating
+    kernel, the reference's included, differs from the float64 truth by up to
+    about sqrt(K) * 2^-24 * mag, so where a dot product cancels to near zero the
+    literal metric (floor 1e-6 max|ref|) measures the cancellation, not the
+    kernel."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    mag = np.broadcast_to(np.asarray(mag, np.float64), want.shape)
+    fin = np.isfinite(want)
+    if not fin.any():
+        return 0.0
+    return float((np.abs(got[fin] - want[fin]) / np.maximum(np.abs(want[fin]), mag[fin])).max())
+
+
 def assert_close(got, want, tol, what=""):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

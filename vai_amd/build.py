@@ -60,8 +60,30 @@ def _build_pymodule():
     return out
 
 
-def _compile(src):
+def _local_headers(src, seen=None):
+    """The quoted #include files src pulls in, transitively."""
+    import re
+    seen = set() if seen is None else seen
+    with open(src) as f:
+        for inc in re.findall(r'^\s*#include\s+"([^"]+)"', f.read(), re.M):
+            h = os.path.normpath(os.path.join(os.path.dirname(src), inc))
+            if os.path.exists(h) and h not in seen:
+                seen.add(h)
+                _local_headers(h, seen)
+    return seen
+
+
+def _stale(src, obj):
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(f) > t for f in [src, *_local_headers(src)])
+
+
+def _compile(src, only_stale=False):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if only_stale and not _stale(src, obj):
+        return obj
     cmd = [HIPCC] + COMMON + DEVICE_FLAGS + ["-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [HIPCC] + COMMON + ["-x", "hip", "-c", src, "-o", obj] + DEVICE_FLAGS
@@ -72,12 +94,14 @@ def _compile(src):
     return obj
 
 
-def build(jobs=None):
+def build(jobs=None, only_stale=False):
+    """Compiles every source (only_stale: only those older than their object
+    or its local headers -- a development shortcut; the default rebuilds all)."""
     os.makedirs(BUILD, exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)), 16)
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s: _compile(s, only_stale), srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp] + objs + ["-Wl,-soname,libvai_amd.so"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -108,5 +132,5 @@ def _build_cpp_programs():
 
 
 if __name__ == "__main__":
-    print(build())
+    print(build(only_stale="--changed" in sys.argv))
     sys.exit(0)

@@ -26,6 +26,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 
 namespace vai_dev {
 
@@ -351,12 +352,10 @@ bool attention_ok(const AttnParams& p)
 template <int D>
 static hipError_t attention_launch_d(const AttnParams& p, hipStream_t s)
 {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)attention_fwd_kernel<D>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, fa::Lds<D>::BYTES);
+    static PerDevice lds_once;
+    {
+        hipError_t e = set_max_lds(lds_once, (const void*)attention_fwd_kernel<D>, fa::Lds<D>::BYTES);
         if (e != hipSuccess) return e;
-        attr = true;
     }
     const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
     const dim3 grid(p.units ? p.units : nqt, p.hq, p.batch);

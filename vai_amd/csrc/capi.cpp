@@ -15,6 +15,7 @@
 #include <algorithm>
 #include "../../include/vai_amd.h"
 #include "kernels.h"
+#include "launch_once.h"
 
 using namespace vai_dev;
 
@@ -204,13 +205,10 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
     return VAI_OK;
 }
 
-vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
+// The launches of one Linear; `a` is checked, `p` its plan, and when the plan
+// needs a workspace, a->workspace holds at least p.workspace bytes.
+static vai_status linear_run(const vai_linear_args* a, const LinearPlan& p, hipStream_t s)
 {
-    vai_status st = check_linear(a);
-    if (st != VAI_OK) return st;
-    hipStream_t s = (hipStream_t)stream;
-    const LinearPlan p = plan_linear(a);
-    if (p.workspace && (!a->workspace || a->workspace_bytes < p.workspace)) return VAI_ERR_WORKSPACE;
 
     if (p.kind == LinearPlan::Slab || p.kind == LinearPlan::SlabThenGate) {
         SlabParams sp{};
@@ -263,6 +261,15 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
                                            a->bias, a->b_dtype, a->bias_repeat, a->residual, a->residual_repeat,
                                            a->epilogue, a->residual_order, a->scalar_scale,
                                            a->gated ? a->N / 2 : 0, a->gate_epilogue, a->N, s));
+}
+
+vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
+{
+    const vai_status st = check_linear(a);
+    if (st != VAI_OK) return st;
+    const LinearPlan p = plan_linear(a);
+    if (p.workspace && (!a->workspace || a->workspace_bytes < p.workspace)) return VAI_ERR_WORKSPACE;
+    return linear_run(a, p, (hipStream_t)stream);
 }
 
 // The packed path needs fp16 I and W and K % 128 == 0, K >= 256 (two K

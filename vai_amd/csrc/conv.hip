@@ -31,6 +31,7 @@
 // then serialize.
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 
 namespace vai_dev {
 
@@ -238,7 +239,8 @@ template <int KS, int NF>
 static hipError_t launch_nf(const ConvParams& p, int x_dt, size_t lds, hipStream_t s)
 {
     auto kern = x_dt == DT_F16 ? conv_kernel<KS, NF, half_t> : conv_kernel<KS, NF, float>;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static PerDevice lds_once[2];
+    hipError_t e = set_max_lds(lds_once[x_dt == DT_F16], (const void*)kern, 160 * 1024);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3((p.co + cv::CO_TILE - 1) / cv::CO_TILE, p.ho, p.batch), dim3(512), lds, s, p);
     return hipGetLastError();

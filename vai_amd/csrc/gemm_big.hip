@@ -34,6 +34,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 #include "tile_store.h"
 
 #define LDS_AS __attribute__((address_space(3)))
@@ -327,23 +328,14 @@ hipError_t gemm_big_launch(const GemmParams& p, bool gated, hipStream_t s)
     const uint32_t tiles_n = gated ? (p.H + big::BN / 2 - 1) / (big::BN / 2) : (p.N + big::BN - 1) / big::BN;
     const size_t lds = (size_t)kBigStages * big::Cfg<kBigBK, kBigStages>::STAGE_BYTES;
     auto kern = gated ? gemm_big_kernel<true, kBigBK, kBigStages> : gemm_big_kernel<false, kBigBK, kBigStages>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[gated]) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set[gated] = true;
-    }
-    // one workgroup per CU at most (the kernel walks its tiles); the CU count
-    // is read once per device
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (!cus[dev]) {
-        hipError_t e = hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-    }
+    static PerDevice lds_once[2];
+    hipError_t e = set_max_lds(lds_once[gated], (const void*)kern, (int)lds);
+    if (e != hipSuccess) return e;
+    // one workgroup per CU at most (the kernel walks its tiles)
+    int cus = 0;
+    if ((e = device_cus(&cus)) != hipSuccess) return e;
     const uint32_t tiles = tiles_m * tiles_n;
-    const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)cus[dev]);
+    const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)cus);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, p);
     return hipGetLastError();
 }

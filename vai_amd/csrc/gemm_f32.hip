@@ -25,6 +25,7 @@
 // range check.
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 
 namespace vai_dev {
 
@@ -253,13 +254,9 @@ template <int NF>
 static hipError_t f32k_launch(const GemmParams& p, hipStream_t s)
 {
     // The ring takes up to 144 KB: above the default dynamic LDS limit.
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)gemm_f32_kernel<NF>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)f32k_lds_bytes<NF>());
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)gemm_f32_kernel<NF>, (int)f32k_lds_bytes<NF>());
+    if (e != hipSuccess) return e;
     const uint32_t tiles = ((p.M + 31) / 32) * ((p.N + 16 * NF - 1) / (16 * NF));
     hipLaunchKernelGGL(gemm_f32_kernel<NF>, dim3(tiles), dim3(256), f32k_lds_bytes<NF>(), s, p);
     return hipGetLastError();

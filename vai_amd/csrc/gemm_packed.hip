@@ -36,6 +36,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 #include "tile_store.h"
 
 #define LDS_AS __attribute__((address_space(3)))
@@ -502,22 +503,13 @@ hipError_t gemm_packed_launch(const GemmParams& p, const void* packed, bool gate
     const uint32_t tiles_m = (p.M + pk::BM - 1) / pk::BM;
     const uint32_t tiles_n = gated ? (p.H + 127) / 128 : (p.N + pk::BN - 1) / pk::BN;
     auto kern = gated ? gemm_packed_kernel<true> : gemm_packed_kernel<false>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[gated]) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)pk::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set[gated] = true;
-    }
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (!cus[dev]) {
-        hipError_t e = hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-    }
+    static PerDevice lds_once[2];
+    hipError_t e = set_max_lds(lds_once[gated], (const void*)kern, (int)pk::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    int cus = 0;
+    if ((e = device_cus(&cus)) != hipSuccess) return e;
     const uint32_t units = tiles_m * tiles_n * (gated ? 1u : std::max<uint32_t>(p.splits, 1));
-    const uint32_t grid = std::min<uint32_t>(units, (uint32_t)cus[dev]);
+    const uint32_t grid = std::min<uint32_t>(units, (uint32_t)cus);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), pk::LDS_BYTES, s, p, (const half_t*)packed);
     return hipGetLastError();
 }

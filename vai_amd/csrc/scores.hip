@@ -21,6 +21,7 @@
 
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 
 #define LDS_AS __attribute__((address_space(3)))
 
@@ -224,13 +225,9 @@ bool scores_fast_ok(const GemmParams& p)
 template <int T>
 static hipError_t scores_launch_t(const GemmParams& p, hipStream_t s)
 {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)scores_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           sc::Tile<T>::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)scores_kernel<T>, sc::Tile<T>::LDS_BYTES);
+    if (e != hipSuccess) return e;
     dim3 grid((p.N + T - 1) / T, (p.M + T - 1) / T, p.batch);
     hipLaunchKernelGGL(scores_kernel<T>, grid, dim3(256), sc::Tile<T>::LDS_BYTES, s, p);
     return hipGetLastError();

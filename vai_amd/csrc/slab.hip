@@ -14,6 +14,7 @@
 // 6*M*R), leaving lane groups that each own one output for the epilogue.
 #include "device_common.h"
 #include "kernels.h"
+#include "launch_once.h"
 
 #include <algorithm>
 
@@ -330,13 +331,9 @@ bool slab_vec_ok(const SlabParams& a)
 hipError_t slab_launch(const SlabParams& a, hipStream_t s)
 {
     if (a.M >= 2 && gemv_mfma_ok(a)) {
-        static bool attr_set = false;   // 64 KB dynamic + the static partial-sum array
-        if (!attr_set) {
-            hipError_t e = hipFuncSetAttribute((const void*)gemv_lds_kernel,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
+        static PerDevice lds_once;   // 64 KB dynamic + the static partial-sum array
+        hipError_t e = set_max_lds(lds_once, (const void*)gemv_lds_kernel, 65536);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL(gemv_lds_kernel, dim3((a.N + 15) / 16), dim3(256), 65536, s, a);
         return hipGetLastError();
     }

@@ -5,7 +5,8 @@
  * (hipMalloc'd, or any device-visible pointer); every launch is asynchronous on
  * the given stream and returns a vai_status (0 = success). Nothing throws
  * across this boundary. The library keeps no per-call state: besides its
- * kernels it holds only per-device launch settings made once (thread-safe).
+ * kernels it holds only per-device launch settings made once (thread-safe),
+ * and the scratch array of vai_linear_launch_noalloc.
  *
  * Callers: the C++ nodes in vai_amd/engine (Linear::run, Convolution::run,
  * AttentionScores::run, GatedMul::run), which replace the reference's
@@ -93,6 +94,19 @@ typedef struct {
 
 vai_status vai_linear_launch(const vai_linear_args* args, vai_stream_t stream);
 size_t vai_linear_workspace_size(const vai_linear_args* args);
+
+/* vai_linear_launch for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. Same arguments, kernels and results as
+ * vai_linear_launch, but args->workspace is ignored: the split-K partials and
+ * the M <= 8 gated intermediate go to a device array inside the library
+ * (VAI_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until the
+ * process ends). Returns VAI_ERR_WORKSPACE when the launch needs more than that
+ * (vai_linear_workspace_size() tells in advance). Nothing is allocated. All
+ * calls on one GPU share its array: calls that overlap in time on that GPU
+ * (two streams, two threads) race on it and must be serialised by the caller. */
+#define VAI_NOALLOC_SCRATCH_BYTES (64u << 20)
+vai_status vai_linear_launch_noalloc(const vai_linear_args* args, vai_stream_t stream);
 
 /* Size of, and the one-time fill of, the packed copy of args->weight that
  * packed_weight takes (0 / VAI_ERR_UNSUPPORTED when the shape or dtypes have

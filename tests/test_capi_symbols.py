@@ -41,6 +41,12 @@ def test_argument_checks_need_no_gpu():
     a.epilogue = 0
     a.gated, a.N = 1, 7
     assert lib.vai_linear_launch(ctypes.byref(a), None) == 1002   # odd 2H
+    assert lib.vai_linear_launch_noalloc(ctypes.byref(a), None) == 1002
+    # a split-K launch whose partials (4 x 4096 x 8192 fp32) exceed the
+    # no-allocation scratch is refused before anything reaches a GPU
+    a.gated, a.M, a.N, a.K, a.split_size = 0, 4096, 8192, 1024, 256
+    assert _capi.linear_workspace_size(a) == 4 * 4096 * 8192 * 4
+    assert lib.vai_linear_launch_noalloc(ctypes.byref(a), None) == 1004
     c = _capi.Conv2dArgs()
     c.out = c.inp = c.weight = 16
     c.batch = c.ci = c.co = c.hi = c.wi = c.stride = 1

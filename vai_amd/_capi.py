@@ -19,6 +19,7 @@ RESIDUAL_ORDERS = {"AFTER_EPILOGUE": 0, "BEFORE_EPILOGUE": 1}
 # Every symbol include/vai_amd.h declares (checked by tests/test_capi_symbols.py).
 EXPORTS = [
     "vai_linear_launch", "vai_linear_workspace_size", "vai_linear_plan", "vai_gated_mul_launch",
+    "vai_linear_launch_noalloc",
     "vai_linear_packed_weight_size", "vai_linear_pack_weight",
     "vai_conv2d_launch", "vai_conv2d_workspace_size", "vai_conv2d_packed_weight_size", "vai_conv2d_pack_weight",
     "vai_attn_scores_launch", "vai_attention_launch", "vai_attention_workspace_size",
@@ -95,6 +96,7 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         vp, sz, u32, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int32
         L.vai_linear_launch.argtypes = [ctypes.POINTER(LinearArgs), vp]
+        L.vai_linear_launch_noalloc.argtypes = [ctypes.POINTER(LinearArgs), vp]
         L.vai_linear_workspace_size.argtypes = [ctypes.POINTER(LinearArgs)]
         L.vai_linear_workspace_size.restype = sz
         L.vai_linear_plan.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_char_p, sz, ctypes.POINTER(u32)]

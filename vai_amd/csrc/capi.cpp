@@ -272,6 +272,44 @@ vai_status vai_linear_launch(const vai_linear_args* a, vai_stream_t stream)
     return linear_run(a, p, (hipStream_t)stream);
 }
 
+// ---- vai_linear_launch_noalloc: the workspace is a file-scope device array.
+// Each device holds its own copy from the library's load until the process
+// ends. Host code must use the address hipGetSymbolAddress returns for the
+// current device, never the array's name (a host-side stand-in).
+static __device__ __align__(256) unsigned char scratch[VAI_NOALLOC_SCRATCH_BYTES];
+
+static hipError_t scratch_address(void** ptr)
+{
+    static PerDevice once;
+    static void* addr[kMaxDevices] = {};
+    const hipError_t e = once.run([](int d) { return hipGetSymbolAddress(&addr[d], HIP_SYMBOL(scratch)); });
+    if (e != hipSuccess) return e;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+    *ptr = addr[dev];
+    return *ptr ? hipSuccess : hipErrorInvalidSymbol;
+}
+
+vai_status vai_linear_launch_noalloc(const vai_linear_args* a, vai_stream_t stream)
+{
+    const vai_status st = check_linear(a);
+    if (st != VAI_OK) return st;
+    const LinearPlan p = plan_linear(a);
+    if (p.workspace > VAI_NOALLOC_SCRATCH_BYTES) return VAI_ERR_WORKSPACE;
+    vai_linear_args b = *a;
+    b.workspace = nullptr;
+    b.workspace_bytes = 0;
+    if (p.workspace) {
+        // Every kernel that uses the workspace writes each element it later
+        // reads (split-K planes, the ungated GEMV output), so the array needs
+        // no clearing between calls.
+        const hipError_t e = scratch_address(&b.workspace);
+        if (e != hipSuccess) return hip_status(e);
+        b.workspace_bytes = VAI_NOALLOC_SCRATCH_BYTES;
+    }
+    return linear_run(&b, p, (hipStream_t)stream);
+}
+
 // The packed path needs fp16 I and W and K % 128 == 0, K >= 256 (two K
 // stages per loop trip, copies at most one tile ahead); the size does not
 // depend on M.

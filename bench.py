@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 ROTATE_BYTES = 384 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.tsv")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "l2_miss_traffic.tsv")
 # rocprofv3 counter scale factors on gfx950, measured with GatedMul over a
 # [4096, 4096] fp32 input (reads exactly 64 MiB, writes 32 MiB): FETCH_SIZE
 # reports half the bytes read, WRITE_SIZE reports the bytes written.
@@ -67,7 +67,8 @@ class Case:
 
 
 def load_traffic():
-    """HBM bytes per launch from the committed rocprofv3 counter table:
+    """L2-miss bytes per launch (HBM plus Infinity Cache hits) from the committed
+    rocprofv3 counter table:
     workload key -> FETCH_FACTOR * FETCH_SIZE + WRITE_FACTOR * WRITE_SIZE, summed
     over the rows of one key (a split-K GEMM and its reduce are one step)."""
     out = {}

@@ -90,6 +90,16 @@ typedef struct {
      * shapes (M > 8, fp16 I and W) then stream W into the matrix cores from
      * that fragment-major copy instead of staging it through LDS. */
     const void* packed_weight;
+    /* Accumulator dtype, Linear::setAccDtype (/root/reference/vai/nodes/
+     * linear.h:289,2320): VAI_DTYPE_F32 (0, the default and the reference's
+     * AMD default) or VAI_DTYPE_F16. F16 applies where the reference's tile
+     * kernel honours it -- M > 8 with at least one fp16 operand -- and then
+     * sums in fp16 in the order of linear-tile.comp:292-320 (4-wide k steps
+     * from each split's start, k+3 first, every fma rounded to fp16), clamps
+     * the sums to +-65504 and finishes in fp32. The GEMV (M <= 8) and fp32 x
+     * fp32 products accumulate in fp32 whatever is asked, as the reference's
+     * do. Split-K only when split_size asks for it. */
+    int32_t acc_dtype;
 } vai_linear_args;
 
 vai_status vai_linear_launch(const vai_linear_args* args, vai_stream_t stream);
@@ -169,11 +179,23 @@ size_t vai_conv2d_packed_weight_size(const vai_conv2d_args* args);
 vai_status vai_conv2d_pack_weight(const vai_conv2d_args* args, void* packed, size_t packed_bytes,
                                   vai_stream_t stream);
 
+/* The reference's MAX_CAUSAL_BLOCKS (/root/reference/vai/shaders/common/
+ * spec_constants.h:35). */
+#define VAI_MAX_CAUSAL_BLOCKS 32
+
 /* ---------------------------------------------------------------------------
  * Attention scores: S[b,h,i,j] = scale * sum_d Q[b,h,i,d] K[b,h/g,j,d],
  * g = Hq/Hkv, fp32 accumulation, S fp32. causal != 0 hides key j from query i
  * when j > i + (Tkv - Tq) (queries align with the keys' end); span > 0 also
  * hides j < i + Tkv - Tq + 1 - span. Hidden entries are -inf.
+ * A block mask (mask_blocks > 0, causal must then be 0) replaces the causal
+ * flag with the reference's list of blocks, each causal or fully visible
+ * (writeCausalMask, /root/reference/vai/nodes/attention.h:40-55): bit
+ * (mask_blocks - 1 - k) of mask_bits marks block k causal, mask_block_end
+ * holds the ends (query rows, increasing) of every block but the last, which
+ * ends at Tq. A query in a causal block sees keys up to itself, one in a full
+ * block sees keys up to its block's end (common/causal_mask.h:25-38): a
+ * prefix-LM mask is {2 blocks, bits 0b01, end {prefix}}.
  * Q [batch,Hq,Tq,D], K [batch,Hkv,Tkv,D], same dtype (f16 or f32).
  * The Q.K^T stage of the reference's attention kernels
  * (/root/reference/vai/shaders/attention.comp:155-182,
@@ -188,6 +210,9 @@ typedef struct {
     float scale;
     uint32_t causal;
     uint32_t span;
+    uint32_t mask_blocks;                                  /* 0: the causal flag alone */
+    uint32_t mask_bits;
+    uint32_t mask_block_end[VAI_MAX_CAUSAL_BLOCKS - 1];
 } vai_attn_scores_args;
 
 vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t stream);
@@ -195,7 +220,7 @@ vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t
 /* ---------------------------------------------------------------------------
  * Attention: O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h/g,j,:] + mask)
  * V[b,h/g,j,:], g = Hq/Hkv, with the mask rule of vai_attn_scores_launch
- * (causal, span). fp32 softmax statistics and accumulation; P is rounded to
+ * (causal, span, or a block mask). fp32 softmax statistics and accumulation; P is rounded to
  * fp16 for the P.V product. Q [batch,Hq,Tq,D], K/V [batch,Hkv,Tkv,D] fp16,
  * D in {64, 128, 256}; O [batch,Hq,Tq,D] in o_dtype (f32 or f16). A query
  * with no visible key gives zeros. Long key ranges may be split over
@@ -217,6 +242,9 @@ typedef struct {
     uint32_t span;
     void* workspace;              /* vai_attention_workspace_size() bytes, or NULL when that is 0 */
     size_t workspace_bytes;
+    uint32_t mask_blocks;                                  /* as vai_attn_scores_args */
+    uint32_t mask_bits;
+    uint32_t mask_block_end[VAI_MAX_CAUSAL_BLOCKS - 1];
 } vai_attention_args;
 
 vai_status vai_attention_launch(const vai_attention_args* args, vai_stream_t stream);

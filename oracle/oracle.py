@@ -32,6 +32,8 @@ def lib():
         _lib.orc_f2h.restype = ctypes.c_uint16
         _lib.orc_h2f.restype = ctypes.c_float
         _lib.orc_num_threads.restype = ctypes.c_int
+        _lib.orc_fma16.restype = ctypes.c_uint16
+        _lib.orc_fma16.argtypes = [ctypes.c_uint16] * 3
     return _lib
 
 
@@ -99,6 +101,33 @@ def linear(inp, weight, bias=None, residual=None, *, epi="NONE", order=0, scale=
     return out
 
 
+def linear_acc16(inp, weight, bias=None, residual=None, *, epi="NONE", order=0, scale=1.0,
+                 out_dtype=np.float32, split_size=0, gated=False, gate_epi="SILU"):
+    """The tile path with an fp16 accumulator (Linear::setAccDtype(Fp16)):
+    fp16 sums in linear-tile.comp's fma order, clamped, finished in fp32."""
+    inp, weight, bias, residual = _c(inp), _c(weight), _c(bias), _c(residual)
+    K, N = weight.shape[-1], weight.shape[0]
+    M = inp.size // K
+    cols = N // 2 if gated else N
+    out = np.empty(inp.shape[:-1] + (cols,), dtype=out_dtype)
+    bias_rep = 0 if bias is None or bias.size == M * N else bias.size
+    res_rep = 0 if residual is None or residual.size == M * N else residual.size
+    lib().orc_linear_acc16(_p(out), _dt(out), _p(inp), _dt(inp), _p(weight), _dt(weight),
+                           _p(bias), _dt(bias), ctypes.c_uint32(bias_rep), _p(residual), ctypes.c_uint32(res_rep),
+                           ctypes.c_uint32(M), ctypes.c_uint32(N), ctypes.c_uint32(K),
+                           ctypes.c_int(EPILOGUES[epi]), ctypes.c_int(order), ctypes.c_float(scale),
+                           ctypes.c_uint32(split_size), ctypes.c_int(1 if gated else 0),
+                           ctypes.c_int(EPILOGUES[gate_epi]))
+    return out
+
+
+def fma16(a, b, c):
+    """fp16 fused multiply-add on fp16 arrays (one rounding), elementwise."""
+    a, b, c = (np.ascontiguousarray(v, np.float16).view(np.uint16) for v in (a, b, c))
+    f = np.vectorize(lambda x, y, z: lib().orc_fma16(int(x), int(y), int(z)), otypes=[np.uint16])
+    return f(a, b, c).view(np.float16)
+
+
 def gemm_f32(a, b):
     """Plain fp32 O = A B^T (CPU baseline kernel)."""
     a = np.ascontiguousarray(a, dtype=np.float32)
@@ -149,8 +178,10 @@ def conv2d(x, weight, bias=None, scale=None, residual=None, *, stride=1, epi="NO
     return out
 
 
-def attn_scores(q, k, *, scale=None, causal=True, span=0):
-    """S = scale * Q K^T per head, -inf where the causal mask hides a key."""
+def attn_scores(q, k, *, scale=None, causal=True, span=0, blocks=None):
+    """S = scale * Q K^T per head, -inf where the mask hides a key. blocks:
+    None, or (bits, ends) -- the reference's block list (len(ends) + 1 blocks,
+    bit (count-1-k) of bits marks block k causal; causal is then ignored)."""
     q, k = _c(q), _c(k)
     assert q.dtype == k.dtype
     Hq, Tq, D = q.shape[-3:]
@@ -159,19 +190,26 @@ def attn_scores(q, k, *, scale=None, causal=True, span=0):
     if scale is None:
         scale = 1.0 / np.sqrt(D)
     out = np.empty(q.shape[:-1] + (Tkv,), dtype=np.float32)
-    lib().orc_attn_scores(_p(out), _p(q), _p(k), _dt(q), ctypes.c_uint32(Hq * lead), ctypes.c_uint32(Hkv * lead),
-                          ctypes.c_uint32(Tq), ctypes.c_uint32(Tkv), ctypes.c_uint32(D),
-                          ctypes.c_float(scale), ctypes.c_int(1 if causal else 0), ctypes.c_uint32(span))
+    nb, bits, ends = 0, 0, None
+    if blocks is not None:
+        bits, e = blocks
+        nb = len(e) + 1
+        ends = np.ascontiguousarray(np.asarray(list(e) + [0], np.uint32))
+        causal = False
+    lib().orc_attn_scores_blocks(_p(out), _p(q), _p(k), _dt(q), ctypes.c_uint32(Hq * lead),
+                                 ctypes.c_uint32(Hkv * lead), ctypes.c_uint32(Tq), ctypes.c_uint32(Tkv),
+                                 ctypes.c_uint32(D), ctypes.c_float(scale), ctypes.c_int(1 if causal else 0),
+                                 ctypes.c_uint32(span), ctypes.c_uint32(nb), ctypes.c_uint32(bits), _p(ends))
     return out
 
 
-def attention(q, k, v, *, scale=None, causal=True, span=0, out_dtype=np.float32):
+def attention(q, k, v, *, scale=None, causal=True, span=0, out_dtype=np.float32, blocks=None):
     """O = softmax(S) V per query row, S = attn_scores(q, k) (the mask's
     -inf entries drop out), in float64 from the fp16 operands; a row with no
     visible key gives 0. The fused pass of attention-fa.comp (scores at
     :581-591, online softmax, P.V), /root/reference/vai/shaders/."""
     q, k, v = _c(q), _c(k), _c(v)
-    S = attn_scores(q, k, scale=scale, causal=causal, span=span).astype(np.float64)
+    S = attn_scores(q, k, scale=scale, causal=causal, span=span, blocks=blocks).astype(np.float64)
     Hq, Tq, D = q.shape[-3:]
     Hkv, Tkv, _ = k.shape[-3:]
     g = Hq // Hkv

@@ -188,6 +188,104 @@ void orc_gemm_f32(float* O, const float* A, const float* Bm, uint32_t M, uint32_
         }
 }
 
+/* ---- fp16 accumulation, Linear::setAccDtype(Fp16) -------------------------
+ * linear-tile.comp:55,71,292-320: the sums are float16; each split walks its
+ * K span in 4-wide steps from the span's start, one step being
+ *   sum = fma(a[k],b[k], fma(a[k+1],b[k+1], fma(a[k+2],b[k+2], fma(a[k+3],b[k+3], sum))))
+ * (k+3 first, each fma rounded once to fp16; elements past the span are 0),
+ * then the sums are clamped to +-65504 (linear-tile.comp:317-321) and folded
+ * in fp32 like any partial (linear-reduce.comp:84-98). Operands are staged
+ * as fp16 (the tile contract: at least one of them is fp16 here). */
+
+/* double -> fp16 bits, IEEE round-to-nearest-even with subnormals kept and
+ * overflow to inf. The fma's exact product a*b (22 significant bits) plus the
+ * fp16 sum is exact in double whenever their exponents lie within 42 of each
+ * other, which holds for all but sums with vanishing terms. */
+uint16_t orc_d2h(double x)
+{
+    const uint16_t sign = signbit(x) ? 0x8000u : 0u;
+    const double a = fabs(x);
+    if (isnan(x)) return 0x7E00u;
+    if (a >= 65520.0) return sign | 0x7C00u;          /* past 65504 + half an ulp (a tie rounds to even: up) */
+    if (a < 6.103515625e-05) {                        /* below 2^-14: subnormal, m * 2^-24 */
+        const double m = nearbyint(a * 16777216.0);
+        return (uint16_t)(sign | (uint16_t)m);        /* m == 1024 is the smallest normal's encoding */
+    }
+    int e;
+    const double f = frexp(a, &e);                    /* a = f 2^e, f in [0.5, 1) */
+    double m = nearbyint(ldexp(f, 11));               /* 11 significant bits */
+    if (m == 2048.0) { m = 1024.0; ++e; }
+    const int E = e + 14;                             /* a = (m/1024) 2^(E-15) */
+    if (E >= 31) return sign | 0x7C00u;
+    return (uint16_t)(sign | (uint16_t)(E << 10) | (uint16_t)((uint32_t)m - 1024u));
+}
+
+/* fp16 fused multiply-add: a*b + c rounded once to fp16 (operands fp16 bits). */
+uint16_t orc_fma16(uint16_t a, uint16_t b, uint16_t c)
+{
+    return orc_d2h((double)orc_h2f(a) * (double)orc_h2f(b) + (double)orc_h2f(c));
+}
+
+/* One split's fp16 sum of a . b over [k0, k1), clamped, as a float. */
+static float acc16_span(const uint16_t* a, const uint16_t* b, uint32_t k0, uint32_t k1)
+{
+    uint16_t sum = 0;
+    for (uint32_t k = k0; k < k1; k += 4)
+        for (int q = 3; q >= 0; --q) {
+            const uint32_t kk = k + (uint32_t)q;
+            sum = orc_fma16(kk < k1 ? a[kk] : 0, kk < k1 ? b[kk] : 0, sum);
+        }
+    const float v = orc_h2f(sum);
+    return fminf(fmaxf(v, -65504.f), 65504.f);
+}
+
+/* O = s*epi(sum_z P_z + B) (+R), P_z the fp16-accumulated split sums; gated:
+ * O[m,j] = gate_epi(g + B[j]) * (u + B[H+j]) over W = [gate rows; up rows]. */
+void orc_linear_acc16(void* O, int oDt, const void* I, int iDt, const void* W, int wDt,
+                      const void* B, int bDt, uint32_t biasRepeat, const void* R, uint32_t residualRepeat,
+                      uint32_t M, uint32_t N, uint32_t K, int epi, int order, float s, uint32_t splitSize,
+                      int gated, int gateEpi)
+{
+    if (splitSize == 0 || splitSize > K) splitSize = K;
+    const uint32_t H = gated ? N / 2 : 0, cols = gated ? H : N;
+    #pragma omp parallel
+    {
+        uint16_t* irow = (uint16_t*)malloc(2 * (size_t)K);
+        uint16_t* w0 = (uint16_t*)malloc(2 * (size_t)K);
+        uint16_t* w1 = (uint16_t*)malloc(2 * (size_t)K);
+        #pragma omp for schedule(static)
+        for (long long mm = 0; mm < (long long)M; ++mm) {
+            const uint32_t m = (uint32_t)mm;
+            for (uint32_t k = 0; k < K; ++k) irow[k] = orc_f2h_ieee(rd(I, iDt, (size_t)m * K + k));
+            for (uint32_t n = 0; n < cols; ++n) {
+                for (uint32_t k = 0; k < K; ++k) {
+                    w0[k] = orc_f2h_ieee(rd(W, wDt, (size_t)n * K + k));
+                    if (gated) w1[k] = orc_f2h_ieee(rd(W, wDt, (size_t)(H + n) * K + k));
+                }
+                if (gated) {
+                    float g = B ? rd(B, bDt, n) : 0.f, u = B ? rd(B, bDt, H + n) : 0.f;
+                    for (uint32_t k0 = 0; k0 < K; k0 += splitSize) {
+                        const uint32_t k1 = k0 + splitSize < K ? k0 + splitSize : K;
+                        g += acc16_span(irow, w0, k0, k1);
+                        u += acc16_span(irow, w1, k0, k1);
+                    }
+                    wr(O, oDt, (size_t)m * H + n, orc_epilogue(g, gateEpi) * u);
+                } else {
+                    const size_t idx = (size_t)m * N + n;
+                    float acc = B ? rd(B, bDt, biasRepeat ? idx % biasRepeat : idx) : 0.f;
+                    for (uint32_t k0 = 0; k0 < K; k0 += splitSize) {
+                        const uint32_t k1 = k0 + splitSize < K ? k0 + splitSize : K;
+                        acc += acc16_span(irow, w0, k0, k1);
+                    }
+                    const float r = R ? rd(R, oDt, residualRepeat ? idx % residualRepeat : idx) : 0.f;
+                    wr(O, oDt, idx, finish(acc, r, epi, order, s));
+                }
+            }
+        }
+        free(irow); free(w0); free(w1);
+    }
+}
+
 /* linear-reduce.comp:80-116: O = s*epi(sum_z P[z] + B) (+R), P and R in oDt. */
 void orc_linear_reduce(void* O, const void* P, int oDt, uint32_t splitCount, uint32_t MN,
                        const void* B, int bDt, uint32_t biasRepeat,
@@ -265,23 +363,42 @@ void orc_conv2d(void* O, int oDt, const void* X, int iDt, const void* W, int wDt
 
 /* ---- Attention scores: the Q.K^T stage of attention.comp:155-182 and
  * attention-fa.comp:581-591. S[h,i,j] = (sum_d Q[h,i,d] K[hk,j,d]) * scale,
- * fp32 accumulation; hk = h / (Hq/Hkv) (GQA). Causal (common/causal_mask.h:
- * 25-42 with one causal block): queries align with the keys' end, so key j is
- * visible to query i iff j <= i + (Tkv - Tq); span > 0 also hides
- * j < pos + 1 - span where pos = i + Tkv - Tq. Hidden entries are -inf. */
-void orc_attn_scores(float* S, const void* Q, const void* Kt, int dt,
-                     uint32_t Hq, uint32_t Hkv, uint32_t Tq, uint32_t Tkv, uint32_t D,
-                     float scale, int causal, uint32_t span)
+ * fp32 accumulation; hk = h / (Hq/Hkv) (GQA). Mask (common/causal_mask.h:
+ * 25-42, attention-fa.comp:135-146 without a KV cache): queries align with
+ * the keys' end, query i at key position pos = i + Tkv - Tq. Its new-token end
+ * comes from the block list -- nBlocks blocks, block k causal iff bit
+ * (nBlocks-1-k) of bits, ends[k] the end row of block k < nBlocks-1 (the last
+ * ends at Tq) -- as i+1 in a causal block and the block's end otherwise (no
+ * blocks: Tq); key j is visible iff j < end + Tkv - Tq. nBlocks == 0 with
+ * causal != 0 is one causal block. span > 0 also hides j < pos + 1 - span.
+ * Hidden entries are -inf. */
+static long long new_token_end(uint32_t t, uint32_t Tq, uint32_t nBlocks, uint32_t bits, const uint32_t* ends)
 {
+    if (nBlocks == 0) return Tq;
+    uint32_t k = 0, e = Tq;
+    while (k + 1 < nBlocks) {
+        const uint32_t b = ends[k] < Tq ? ends[k] : Tq;
+        if (t < b) { e = b; break; }
+        ++k;
+    }
+    return ((bits >> (nBlocks - 1 - k)) & 1u) ? (long long)t + 1 : (long long)e;
+}
+
+void orc_attn_scores_blocks(float* S, const void* Q, const void* Kt, int dt,
+                            uint32_t Hq, uint32_t Hkv, uint32_t Tq, uint32_t Tkv, uint32_t D,
+                            float scale, int causal, uint32_t span, uint32_t nBlocks, uint32_t bits,
+                            const uint32_t* ends)
+{
+    if (nBlocks == 0 && causal) { nBlocks = 1; bits = 1; }
     const uint32_t group = Hq / Hkv;
     #pragma omp parallel for schedule(static) collapse(2)
     for (long long h = 0; h < (long long)Hq; ++h)
         for (long long i = 0; i < (long long)Tq; ++i) {
             const uint32_t hk = (uint32_t)h / group;
             const long long pos = i + (long long)Tkv - (long long)Tq;
+            const long long kend = new_token_end((uint32_t)i, Tq, nBlocks, bits, ends) + (long long)Tkv - (long long)Tq;
             for (uint32_t j = 0; j < Tkv; ++j) {
-                int visible = 1;
-                if (causal && (long long)j > pos) visible = 0;
+                int visible = (long long)j < kend;
                 if (span && pos >= (long long)span && (long long)j < pos + 1 - (long long)span) visible = 0;
                 float acc = 0.f;
                 if (visible)
@@ -290,6 +407,13 @@ void orc_attn_scores(float* S, const void* Q, const void* Kt, int dt,
                 S[((size_t)h * Tq + i) * Tkv + j] = visible ? acc * scale : -INFINITY;
             }
         }
+}
+
+void orc_attn_scores(float* S, const void* Q, const void* Kt, int dt,
+                     uint32_t Hq, uint32_t Hkv, uint32_t Tq, uint32_t Tkv, uint32_t D,
+                     float scale, int causal, uint32_t span)
+{
+    orc_attn_scores_blocks(S, Q, Kt, dt, Hq, Hkv, Tq, Tkv, D, scale, causal, span, 0, 0, NULL);
 }
 
 int orc_num_threads(void)

@@ -40,6 +40,25 @@ def test_attention(gpu, b, hq, hkv, tq, tkv, d, causal, span, odt):
         np.testing.assert_array_equal(got[..., : tq - tkv, :], 0.0)
 
 
+@pytest.mark.parametrize("hq, hkv, tq, tkv, d, blocks, span", [
+    (4, 2, 300, 300, 128, (0b01, [120]), 0),          # prefix-LM over a causal tail
+    (2, 2, 257, 257, 64, (0b101, [70, 190]), 0),      # causal / full / causal
+    (2, 1, 200, 260, 256, (0b010, [50, 130]), 60),    # full / causal / full, Tq < Tkv, window
+    (2, 2, 64, 1000, 64, (0b10, [20]), 0),            # one query tile, key split and merge
+])
+def test_attention_block_mask(gpu, hq, hkv, tq, tkv, d, blocks, span):
+    rng = np.random.default_rng(tq + d)
+    q = draw((1, hq, tq, d), rng, np.float16)
+    k = draw((1, hkv, tkv, d), rng, np.float16)
+    v = draw((1, hkv, tkv, d), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    out = gpu.DeviceArray((1, hq, tq, d), np.float32)
+    print(f"attention blocks={blocks} hq={hq} hkv={hkv} tq={tq} tkv={tkv} d={d} span={span}", flush=True)
+    got = gpu.attention(out, D(q), D(k), D(v), blocks=blocks, span=span).numpy()
+    want = oracle.attention(q, k, v, blocks=blocks, span=span, out_dtype=np.float32)
+    assert_close(got, want, FP16)
+
+
 def test_attention_rejects(gpu):
     """fp32 inputs and head dims other than 64/128/256 are refused."""
     import ctypes

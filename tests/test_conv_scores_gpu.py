@@ -123,6 +123,34 @@ def test_scores(gpu, hq, hkv, tq, tkv, d, causal, span, dt):
     assert_close(got, want, FP32 if dt == np.float16 else TRANS)
 
 
+@pytest.mark.parametrize("tq, tkv, d, blocks, span, dt", [
+    (300, 300, 64, (0b01, [100]), 0, np.float16),            # prefix-LM, fast kernel, ragged tiles
+    (257, 257, 128, (0b101, [70, 190]), 0, np.float16),      # causal / full / causal
+    (200, 260, 64, (0b010, [50, 130]), 40, np.float16),      # full / causal / full, Tq < Tkv, window
+    (90, 90, 48, (0b01, [33]), 0, np.float32),               # the generic tile path
+    (128, 128, 64, (0b0, []), 0, np.float16),                # one full block: no mask
+])
+def test_scores_block_mask(gpu, tq, tkv, d, blocks, span, dt):
+    rng = np.random.default_rng(tq)
+    q = draw((2, tq, d), rng, dt)
+    k = draw((2, tkv, d), rng, dt)
+    print(f"scores blocks={blocks} tq={tq} tkv={tkv} d={d}", flush=True)
+    got = run_scores(gpu, q, k, blocks=blocks, span=span)
+    want = oracle.attn_scores(q, k, blocks=blocks, span=span)
+    assert_close(got, want, FP32 if dt == np.float16 else TRANS)
+
+
+def test_scores_block_mask_rejects(gpu):
+    import ctypes
+    D = gpu.DeviceArray
+    q = D((1, 16, 64), np.float16)
+    a = gpu.attn_scores_args(D((1, 16, 16), np.float32), q, q, blocks=(0b01, [8, 4]))   # ends must increase
+    assert gpu.lib().vai_attn_scores_launch(ctypes.byref(a), None) == 1001
+    a = gpu.attn_scores_args(D((1, 16, 16), np.float32), q, q, blocks=(0b01, [8]))
+    a.causal = 1                                                                         # both at once
+    assert gpu.lib().vai_attn_scores_launch(ctypes.byref(a), None) == 1001
+
+
 def test_config4_attention_scores(gpu):
     """Q,K [8,1024,256] fp16, S = QK^T/16 causal; oracle on heads 0 and 7."""
     rng = np.random.default_rng(0)

@@ -175,6 +175,28 @@ def test_attention_node(gpu, hq, hkv, tq, tkv, d, causal, span):
     assert_close(got, oracle.attention(q, k, v, causal=causal, span=span, out_dtype=np.float32), FP16)
 
 
+def test_attention_node_block_mask(gpu):
+    """setCausalMask on the Attention and AttentionScores nodes: a prefix-LM
+    mask, then a three-block mask set after the first forward (re-records)."""
+    pv = pyvai()
+    rng = np.random.default_rng(5)
+    hq, tq, d = 2, 150, 64
+    q = draw((1, hq, tq, d), rng, np.float16)
+    k = draw((1, hq, tq, d), rng, np.float16)
+    v = draw((1, hq, tq, d), rng, np.float16)
+    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d), ["Q", "K", "V"], {})
+    net.node.set_causal_mask(0b01, [40])
+    got = forward(net, {"Q": q, "K": k, "V": v})
+    assert_close(got, oracle.attention(q, k, v, blocks=(0b01, [40]), out_dtype=np.float32), FP16)
+    net.node.set_causal_mask(0b101, [30, 90], span=70)
+    got = forward(net, {"Q": q, "K": k, "V": v})
+    assert_close(got, oracle.attention(q, k, v, blocks=(0b101, [30, 90]), span=70, out_dtype=np.float32), FP16)
+    sn = build_net(lambda: pv.nodes.AttentionScoresNode(num_q_heads=hq, head_dim=d), ["in0", "K"], {})
+    sn.node.set_causal_mask(0b01, [40])
+    got = forward(sn, {"in0": q[0], "K": k[0]})
+    assert_close(got, oracle.attn_scores(q[0], k[0], blocks=(0b01, [40])), FP32)
+
+
 def test_gpt2_cfc_through_the_engine(gpu):
     """BASELINE config 1 via input - linear - output."""
     import os, sys
@@ -237,3 +259,23 @@ def test_gated_ffn_packed_fusion(gpu):
     want = oracle.gated_mul(oracle.linear(x[rows], w, stage="tile"), epi="SILU")
     assert_close(outs[True][rows], want, TRANS)
     assert_close(outs[False][rows], want, TRANS)
+
+
+def test_linear_node_acc16(gpu):
+    """Linear::setAccDtype(Fp16) through the engine: the node's plan switches to
+    the fp16-accumulating kernel and its output equals the oracle's fma chain."""
+    pv = pyvai()
+    rng = np.random.default_rng(0)
+    m, k, n = 40, 320, 72
+    w = draw(normal((n, k), 0.05), rng, np.float16)
+    b = draw((n,), rng)
+    x = draw((m, k), rng, np.float16)
+    net = build_net(lambda: pv.nodes.LinearNode(in_dim=k, out_dim=n), ["in0"], {"weight": w, "bias": b}, w_dtype="F16")
+    net.set_acc_dtype(net.node, pv.Dtype.F16)
+    got = forward(net, {"in0": x})
+    assert net.node.plan == "tile_acc16_64x64"
+    assert np.array_equal(got, oracle.linear_acc16(x, w, b))
+    net.set_acc_dtype(net.node, pv.Dtype.F32)   # back to fp32: re-records with the MFMA tile
+    got = forward(net, {"in0": x})
+    assert net.node.plan.startswith("tile_f16")
+    assert_close(got, oracle.linear(x, w, b, stage="tile"), FP32)

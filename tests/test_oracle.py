@@ -271,3 +271,149 @@ def test_attention_oracle_pins():
     q4, k4, v4 = _attn_inputs(rng, 1, 1, 5, 3, 8)
     o = oracle.attention(q4, k4, v4, causal=True, out_dtype=np.float64)[0, 0]
     np.testing.assert_array_equal(o[:2], 0.0)
+
+
+# ---- fp16 accumulation (Linear::setAccDtype(Fp16), linear-tile.comp:292-320) --
+
+def _round_half_exact(fr):
+    """An exact rational rounded to fp16 (IEEE RNE, subnormals, overflow -> inf),
+    written independently of the oracle's double-based rounding."""
+    from fractions import Fraction
+    if fr == 0:
+        return np.float16(0.0)
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    quantum = Fraction(2) ** (max(e, -14) - 10)
+    n = round(a / quantum)            # Fraction rounding: ties to even
+    v = n * quantum
+    if v >= 65536:
+        return np.float16(sign * np.inf)
+    return np.float16(sign * float(v))
+
+
+def _fma16_exact(a, b, c):
+    from fractions import Fraction
+    return _round_half_exact(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def test_fma16_against_exact_rationals():
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal(3000).astype(np.float16)
+    b = (rng.standard_normal(3000) * np.exp2(rng.integers(-12, 8, 3000))).astype(np.float16)
+    c = (rng.standard_normal(3000) * np.exp2(rng.integers(-20, 12, 3000))).astype(np.float16)
+    got = oracle.fma16(a, b, c)
+    want = np.array([_fma16_exact(x, y, z) for x, y, z in zip(a, b, c)], np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    h = np.float16
+    # one rounding, not two: (1 + 2^-10)(1 - 2^-10) - 1 = -2^-20 (a subnormal half)
+    assert oracle.fma16([h(1 + 2 ** -10)], [h(1 - 2 ** -10)], [h(-1)])[0] == h(-(2.0 ** -20))
+    # ties to even: 1 + 2^-11 -> 1, (1 + 2^-10) + 2^-11 -> 1 + 2^-9
+    assert oracle.fma16([h(2 ** -6)], [h(2 ** -5)], [h(1)])[0] == h(1)
+    assert oracle.fma16([h(2 ** -6)], [h(2 ** -5)], [h(1 + 2 ** -10)])[0] == h(1 + 2 ** -9)
+    # overflow: 65504 + 16 is a tie that rounds to inf; 65504 + 15 stays
+    assert np.isposinf(oracle.fma16([h(16)], [h(1)], [h(65504)])[0])
+    assert oracle.fma16([h(15)], [h(1)], [h(65504)])[0] == h(65504)
+
+
+def _acc16_brute(x, w, split):
+    """The fma chain of linear-tile.comp, by exact rationals, tiny shapes only."""
+    M, K = x.shape
+    N = w.shape[0]
+    x16, w16 = x.astype(np.float16), w.astype(np.float16)
+    out = np.zeros((M, N), np.float32)
+    for m in range(M):
+        for n in range(N):
+            tot = np.float32(0)
+            for k0 in range(0, K, split):
+                k1 = min(K, k0 + split)
+                s = np.float16(0)
+                for k in range(k0, k1, 4):
+                    for q in (3, 2, 1, 0):
+                        kk = k + q
+                        s = _fma16_exact(x16[m, kk] if kk < k1 else 0, w16[n, kk] if kk < k1 else 0, s)
+                s = np.float32(min(max(float(s), -65504.0), 65504.0))
+                tot = np.float32(tot + s)
+            out[m, n] = tot
+    return out
+
+
+@pytest.mark.parametrize("k, split", [(9, 9), (13, 8), (32, 32), (40, 12)])
+def test_linear_acc16_brute_force(k, split):
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((3, k)).astype(np.float16)
+    w = (rng.standard_normal((4, k)) * 3).astype(np.float16)
+    got = oracle.linear_acc16(x, w, split_size=split)
+    assert np.array_equal(got, _acc16_brute(x, w, split))
+
+
+def test_linear_acc16_order_clamp_and_error_bound():
+    h = np.float16
+    # within a 4-step k+3 comes first: -2048 + 1 + 1 + 2048 = 2 (ascending order would give 0)
+    x = np.ones((1, 4), h)
+    assert oracle.linear_acc16(x, np.array([[2048, 1, 1, -2048]], h))[0, 0] == 2.0
+    # the 4-steps go up in k: 2048 first, then +1 +1 at 2048's spacing of 2 stay 2048
+    x = np.ones((1, 8), h)
+    w = np.array([[0, 0, 0, 2048, 1, 1, 0, 0]], h)
+    assert oracle.linear_acc16(x, w)[0, 0] == 2048.0
+    # overflowing sums clamp to +-65504, then the fp32 bias is added
+    x = np.full((2, 8), 100, h)
+    w = np.array([np.full(8, 100), np.full(8, -100)], h)
+    got = oracle.linear_acc16(x, w, np.array([0.5, -0.5], np.float32))
+    assert (got == np.array([65504.5, -65504.5], np.float32)).all()
+    # random data: within the fp16 accumulation bound of the float64 result
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((20, 300)).astype(h)
+    w = (rng.standard_normal((30, 300)) * 0.1).astype(h)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    err = np.abs(oracle.linear_acc16(x, w) - exact)
+    assert (err <= 300 * 2.0 ** -11 * mag).all()
+    assert err.max() > 10 * np.abs(oracle.linear(x, w, stage="tile") - exact).max()   # really fp16 sums
+
+
+# ---- block masks (writeCausalMask, attention.h:40-55; causal_mask.h:25-38) ----
+
+def _visible_literal(rows):
+    """Rows of the visibility matrix written out by hand: a list of key ends
+    (exclusive) per query, from key 0 (no span)."""
+    tkv = max(rows)
+    return np.array([[j < e for j in range(tkv)] for e in rows])
+
+
+@pytest.mark.parametrize("tq, tkv, blocks, ends_per_row", [
+    # prefix-LM: rows 0-3 read the whole 4-token prefix, then causal
+    (10, 10, (0b01, [4]), [4, 4, 4, 4, 5, 6, 7, 8, 9, 10]),
+    # causal / full / causal with ends 3 and 7
+    (10, 10, (0b101, [3, 7]), [1, 2, 3, 7, 7, 7, 7, 8, 9, 10]),
+    # full / causal / full
+    (9, 9, (0b010, [2, 5]), [2, 2, 3, 4, 5, 9, 9, 9, 9]),
+    # fewer queries than keys: queries sit at the keys' end (offset 6)
+    (4, 10, (0b01, [2]), [8, 8, 9, 10]),
+    # one causal block is the plain causal mask; ends past Tq are clipped
+    (6, 6, (0b1, []), [1, 2, 3, 4, 5, 6]),
+    (6, 6, (0b01, [20]), [6, 6, 6, 6, 6, 6]),
+    (6, 6, (0b10, [20]), [1, 2, 3, 4, 5, 6]),
+])
+def test_scores_block_masks(tq, tkv, blocks, ends_per_row):
+    rng = np.random.default_rng(tq + tkv)
+    q = rng.standard_normal((2, tq, 8)).astype(np.float16)
+    k = rng.standard_normal((2, tkv, 8)).astype(np.float16)
+    got = oracle.attn_scores(q, k, scale=0.5, blocks=blocks)
+    vis = _visible_literal(ends_per_row)
+    assert vis.shape == (tq, tkv)
+    assert np.array_equal(np.isfinite(got), np.broadcast_to(vis, got.shape))
+    want = np.einsum("hid,hjd->hij", q.astype(np.float64), k.astype(np.float64)) * 0.5
+    np.testing.assert_allclose(got[:, vis], want[:, vis], rtol=1e-5, atol=1e-5)
+    if blocks == (0b1, []):
+        assert np.array_equal(got, oracle.attn_scores(q, k, scale=0.5, causal=True))
+    # a span still cuts from below
+    got = oracle.attn_scores(q, k, scale=0.5, blocks=blocks, span=2)
+    pos = np.arange(tq) + tkv - tq
+    lo = np.where(pos >= 2, pos - 1, 0)
+    vis2 = vis & (np.arange(tkv)[None, :] >= lo[:, None])
+    assert np.array_equal(np.isfinite(got[0]), vis2)

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libvai_amd.so")
 F32, F16, NONE = 0, 1, 2
 EPILOGUES = {"NONE": 0, "RELU": 1, "GELU": 2, "GELU_TANH": 3, "SILU": 4, "SIGMOID": 5}
 RESIDUAL_ORDERS = {"AFTER_EPILOGUE": 0, "BEFORE_EPILOGUE": 1}
+MAX_CAUSAL_BLOCKS = 32
 
 # Every symbol include/vai_amd.h declares (checked by tests/test_capi_symbols.py).
 EXPORTS = [
@@ -43,7 +44,7 @@ class LinearArgs(ctypes.Structure):
         ("bias_repeat", ctypes.c_uint32), ("residual_repeat", ctypes.c_uint32),
         ("scalar_scale", ctypes.c_float), ("split_size", ctypes.c_uint32),
         ("gated", ctypes.c_uint32), ("gate_epilogue", ctypes.c_uint32),
-        ("packed_weight", ctypes.c_void_p),
+        ("packed_weight", ctypes.c_void_p), ("acc_dtype", ctypes.c_int32),
     ]
 
 
@@ -67,6 +68,8 @@ class AttnScoresArgs(ctypes.Structure):
         ("tq", ctypes.c_uint32), ("tkv", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
         ("dtype", ctypes.c_int32), ("scale", ctypes.c_float), ("causal", ctypes.c_uint32),
         ("span", ctypes.c_uint32),
+        ("mask_blocks", ctypes.c_uint32), ("mask_bits", ctypes.c_uint32),
+        ("mask_block_end", ctypes.c_uint32 * (MAX_CAUSAL_BLOCKS - 1)),
     ]
 
 
@@ -78,6 +81,8 @@ class AttentionArgs(ctypes.Structure):
         ("tq", ctypes.c_uint32), ("tkv", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
         ("scale", ctypes.c_float), ("causal", ctypes.c_uint32), ("span", ctypes.c_uint32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("mask_blocks", ctypes.c_uint32), ("mask_bits", ctypes.c_uint32),
+        ("mask_block_end", ctypes.c_uint32 * (MAX_CAUSAL_BLOCKS - 1)),
     ]
 
 
@@ -202,7 +207,7 @@ def _ptr(d):
 
 
 def linear_args(out, inp, weight, bias=None, residual=None, *, epi="NONE", order="AFTER_EPILOGUE",
-                scale=1.0, split_size=0, gated=False, gate_epi="SILU", workspace=None):
+                scale=1.0, split_size=0, gated=False, gate_epi="SILU", workspace=None, acc=np.float32):
     K = weight.shape[-1]
     N = weight.shape[0]
     M = int(np.prod(inp.shape[:-1]))
@@ -225,6 +230,7 @@ def linear_args(out, inp, weight, bias=None, residual=None, *, epi="NONE", order
     a.split_size = split_size
     a.gated = 1 if gated else 0
     a.gate_epilogue = EPILOGUES[gate_epi]
+    a.acc_dtype = dtype_code(acc)
     if workspace is not None:
         a.workspace, a.workspace_bytes = workspace.ptr, workspace.nbytes
     a._keep = (out, inp, weight, bias, residual, workspace)   # the buffers live as long as the args
@@ -327,7 +333,20 @@ def conv2d(out, inp, weight, bias=None, scale=None, residual=None, stream=None, 
     return out
 
 
-def attn_scores_args(scores, q, k, *, scale=None, causal=True, span=0):
+def _set_blocks(a, blocks):
+    """blocks: None, or (bits, ends) -- the reference's block list: len(ends)+1
+    blocks, bit (count-1-k) of bits marks block k causal, ends in query rows."""
+    if blocks is None:
+        return
+    bits, ends = blocks
+    a.causal = 0
+    a.mask_blocks = len(ends) + 1
+    a.mask_bits = bits
+    for i, e in enumerate(ends):
+        a.mask_block_end[i] = e
+
+
+def attn_scores_args(scores, q, k, *, scale=None, causal=True, span=0, blocks=None):
     Hq, Tq, D = q.shape[-3:]
     Hkv, Tkv, _ = k.shape[-3:]
     a = AttnScoresArgs()
@@ -338,6 +357,7 @@ def attn_scores_args(scores, q, k, *, scale=None, causal=True, span=0):
     a.scale = float(1.0 / np.sqrt(D)) if scale is None else float(scale)
     a.causal = 1 if causal else 0
     a.span = span
+    _set_blocks(a, blocks)
     a._keep = (scores, q, k)
     return a
 
@@ -349,7 +369,7 @@ def attn_scores(scores, q, k, stream=None, **kw):
     return scores
 
 
-def attention_args(out, q, k, v, *, scale=None, causal=True, span=0):
+def attention_args(out, q, k, v, *, scale=None, causal=True, span=0, blocks=None):
     Hq, Tq, D = q.shape[-3:]
     Hkv, Tkv, _ = k.shape[-3:]
     a = AttentionArgs()
@@ -360,6 +380,7 @@ def attention_args(out, q, k, v, *, scale=None, causal=True, span=0):
     a.scale = 0.0 if scale is None else float(scale)
     a.causal = 1 if causal else 0
     a.span = span
+    _set_blocks(a, blocks)
     a._keep = (out, q, k, v)
     return a
 

@@ -45,11 +45,8 @@ typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 // The 64-key tiles query tile qt can see: [tb, te).
 __host__ __device__ inline void fa_tile_range(const AttnParams& p, uint32_t qt, int64_t& tb, int64_t& te)
 {
-    const int64_t off = (int64_t)p.tkv - (int64_t)p.tq, q0 = (int64_t)qt * fa::BQ;
-    int64_t kend = (int64_t)p.tkv;
-    if (p.causal) kend = std::min<int64_t>(kend, q0 + fa::BQ - 1 + off + 1);
-    int64_t kbeg = 0;
-    if (p.span) kbeg = std::max<int64_t>(0, q0 + off + 1 - (int64_t)p.span);
+    const uint32_t q0 = qt * fa::BQ, q1 = std::min<uint32_t>(q0 + fa::BQ, p.tq) - 1;
+    const int64_t kend = p.mask.key_end(q1), kbeg = p.mask.key_start(q0);
     tb = kbeg / fa::BKV;
     te = kend <= kbeg ? tb : (kend + fa::BKV - 1) / fa::BKV;
 }
@@ -98,7 +95,6 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
     const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
     const half_t* K = (const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D;
     const half_t* V = (const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * D;
-    const int64_t off = (int64_t)Tkv - (int64_t)Tq;   // query i sits at key position i + off
 
     // this wave's 16 query rows as the B operand of S^T = K Q^T
     const uint32_t qrow = q0 + wave * 16 + lr;
@@ -118,7 +114,9 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
     const int64_t kbeg = tb * BKV, kend = std::min<int64_t>(te * BKV, (int64_t)Tkv);
 
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
-    const int64_t qpos = (int64_t)qrow + off;
+    // this lane's query row reads keys [row_kbeg, row_kend)
+    const uint32_t qclip = qrow < Tq ? qrow : Tq - 1;
+    const int64_t row_kend = p.mask.key_end(qclip), row_kbeg = p.mask.key_start(qclip);
     float m = -__builtin_inff(), l = 0.f;
     float4v o[DB];
 #pragma unroll
@@ -183,8 +181,7 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t kpos = j0 + 16 * f + 4 * lg + r;
-                const bool hide = kpos >= (int64_t)Tkv || (p.causal && kpos > qpos) ||
-                                  (p.span && kpos < qpos + 1 - (int64_t)p.span);
+                const bool hide = kpos >= row_kend || kpos < row_kbeg;
                 const float v = hide ? -__builtin_inff() : st[f][r] * sl2;
                 st[f][r] = v;
                 tmax = fmaxf(tmax, v);

@@ -28,7 +28,7 @@ size_t dtype_bytes(int32_t d) { return d == VAI_DTYPE_F16 ? 2 : 4; }
 vai_status hip_status(hipError_t e) { return e == hipSuccess ? VAI_OK : (vai_status)e; }
 
 struct LinearPlan {
-    enum Kind { Slab, SlabThenGate, Tile, BigTile, PackedTile, F32Small } kind;
+    enum Kind { Slab, SlabThenGate, Tile, BigTile, PackedTile, F32Small, Acc16Tile } kind;
     GemmTile tile;
     uint32_t bm, bn;
     uint32_t split_size, splits;
@@ -52,6 +52,8 @@ vai_status check_linear(const vai_linear_args* a)
     if (a->residual && a->residual_repeat && (a->residual_repeat % a->N != 0 || MN % a->residual_repeat != 0))
         return VAI_ERR_SHAPE;
     if (a->split_size && a->split_size < 32) return VAI_ERR_INVALID_ARG;
+    if (a->acc_dtype != VAI_DTYPE_F32 && a->acc_dtype != VAI_DTYPE_F16 && a->acc_dtype != VAI_DTYPE_NONE)
+        return VAI_ERR_DTYPE;
     if (a->gated) {
         if (a->N % 2 != 0 || a->gate_epilogue > VAI_EPI_SIGMOID) return VAI_ERR_SHAPE;
         if (a->epilogue != VAI_EPI_NONE || a->residual || a->scalar_scale != 1.0f) return VAI_ERR_UNSUPPORTED;
@@ -69,6 +71,14 @@ LinearPlan plan_linear(const vai_linear_args* a)
         p.splits = 1;
         p.split_size = K;
         p.workspace = a->gated ? (size_t)M * N * 4 : 0;
+        return p;
+    }
+    if (a->acc_dtype == VAI_DTYPE_F16 && !(a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32)) {
+        // fp16 accumulation in the reference's order; split only on request
+        p.kind = LinearPlan::Acc16Tile;
+        p.split_size = a->split_size ? a->split_size : K;
+        p.splits = (K + p.split_size - 1) / p.split_size;
+        p.workspace = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
         return p;
     }
     p.kind = LinearPlan::Tile;
@@ -190,6 +200,8 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
         sp.M = a->M;
         snprintf(buf, sizeof buf, "%s%s", (sp.M >= 2 && gemv_mfma_ok(sp)) ? "slab_mfma" : slab_vec_ok(sp) ? "slab" : "slab_scalar",
                  p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
+    } else if (p.kind == LinearPlan::Acc16Tile) {
+        snprintf(buf, sizeof buf, "tile_acc16_64x64%s", a->gated ? "_gated" : "");
     } else if (p.kind == LinearPlan::F32Small) {
         snprintf(buf, sizeof buf, "tile_f32_32x%u_kwaves", p.bn);
     } else if (p.kind == LinearPlan::BigTile || p.kind == LinearPlan::PackedTile) {
@@ -252,6 +264,15 @@ static vai_status linear_run(const vai_linear_args* a, const LinearPlan& p, hipS
                                                0, a->N, s));
     }
     if (p.kind == LinearPlan::BigTile) return hip_status(gemm_big_launch(g, a->gated != 0, s));
+    if (p.kind == LinearPlan::Acc16Tile) {
+        hipError_t e = gemm_acc16_launch(g, a->gated != 0, s);
+        if (e != hipSuccess || p.splits == 1) return hip_status(e);
+        return hip_status(linear_reduce_launch(a->out, a->o_dtype, (const float*)a->workspace, p.splits,
+                                               (size_t)a->M * (a->gated ? a->N / 2 : a->N), a->bias, a->b_dtype,
+                                               a->bias_repeat, a->residual, a->residual_repeat, a->epilogue,
+                                               a->residual_order, a->scalar_scale, a->gated ? a->N / 2 : 0,
+                                               a->gate_epilogue, a->N, s));
+    }
     if (p.kind == LinearPlan::F32Small) return hip_status(gemm_f32_launch(g, (int)(p.bn / 16), s));
     hipError_t e = gemm_launch(g, a->gated ? BKind::Gated : BKind::Dense,
                                a->gated ? EpiKind::Gated : EpiKind::Linear, p.tile, s);
@@ -335,6 +356,34 @@ vai_status vai_linear_pack_weight(const vai_linear_args* a, void* packed, size_t
                                        (hipStream_t)stream));
 }
 
+// The kernels' mask rule from the causal flag or a block list; checks the list
+// as writeCausalMask does (attention.h:46-55): at most 32 blocks, ends
+// increasing and nonzero.
+static vai_status make_mask(MaskRule& m, uint32_t tq, uint32_t tkv, uint32_t causal, uint32_t span,
+                            uint32_t blocks, uint32_t bits, const uint32_t* ends)
+{
+    m = MaskRule{};
+    m.tq = tq; m.tkv = tkv; m.span = span;
+    if (blocks == 0) {
+        m.blocks = causal ? 1 : 0;
+        m.bits = 1;
+        return VAI_OK;
+    }
+    if (causal || blocks > VAI_MAX_CAUSAL_BLOCKS) return VAI_ERR_INVALID_ARG;
+    for (uint32_t k = 0; k + 1 < blocks; ++k) {
+        if (ends[k] == 0 || (k > 0 && ends[k] <= ends[k - 1])) return VAI_ERR_INVALID_ARG;
+        m.end[k] = ends[k];
+    }
+    if (blocks == 1) {   // one block: causal or no mask at all
+        m.blocks = bits & 1u;
+        m.bits = 1;
+        return VAI_OK;
+    }
+    m.blocks = blocks;
+    m.bits = blocks == 32 ? bits : bits & ((1u << blocks) - 1);
+    return VAI_OK;
+}
+
 static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
 {
     if (!a || !a->q || !a->k || !a->v) return VAI_ERR_INVALID_ARG;
@@ -345,7 +394,11 @@ static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
     p.out = a->out; p.q = a->q; p.k = a->k; p.v = a->v; p.o_dtype = a->o_dtype;
     p.batch = a->batch; p.hq = a->hq; p.hkv = a->hkv; p.tq = a->tq; p.tkv = a->tkv; p.head_dim = a->head_dim;
     p.scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)a->head_dim);
-    p.causal = a->causal; p.span = a->span;
+    p.span = a->span;
+    if (vai_status st = make_mask(p.mask, a->tq, a->tkv, a->causal, a->span, a->mask_blocks, a->mask_bits,
+                                  a->mask_block_end); st != VAI_OK)
+        return st;
+    p.causal = p.mask.blocks == 1;
     if (!attention_ok(p)) return VAI_ERR_UNSUPPORTED;
     // Split the key ranges (chunks of 4 tiles = 256 keys) only when the query
     // tiles alone leave CUs idle.
@@ -490,6 +543,10 @@ vai_status vai_attn_scores_launch(const vai_attn_scores_args* a, vai_stream_t st
     g.split_size = g.K; g.splits = 1;
     g.scalar_scale = a->scale; g.causal = a->causal; g.span = a->span;
     g.causal_offset = (int32_t)a->tkv - (int32_t)a->tq;
+    if (vai_status st = make_mask(g.mask, a->tq, a->tkv, a->causal, a->span, a->mask_blocks, a->mask_bits,
+                                  a->mask_block_end); st != VAI_OK)
+        return st;
+    g.causal = g.mask.blocks == 1;   // the diagonal fast path's flag (a block list takes the general one)
     if (scores_fast_ok(g)) return hip_status(scores_launch(g, (hipStream_t)stream));
     const GemmTile t = tiles_of(g.M, g.N, 128, 128) * g.batch >= kCUs ? GemmTile::T128x128 : GemmTile::T64x64;
     return hip_status(gemm_launch(g, BKind::Dense, EpiKind::Scores, t, (hipStream_t)stream));

@@ -46,15 +46,18 @@ __global__ __launch_bounds__(256) void linear_reduce4_kernel(
 {
     const size_t stride = (size_t)gridDim.x * blockDim.x * 4;
     for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < MN; i += stride) {
-        float4v acc = (float4v)0.f;
-        for (uint32_t z = 0; z < splits; ++z) acc += *(const float4v*)(P + (size_t)z * MN + i);
+        // the bias first, then the planes in split order (linear-reduce.comp:90-93)
         const size_t bi = bias_rep ? i % bias_rep : i, ri = res_rep ? i % res_rep : i;
+        float4v acc = (float4v)0.f;
+        if (bias)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = ld(bias, b_dt, bi + k);
+        for (uint32_t z = 0; z < splits; ++z) acc += *(const float4v*)(P + (size_t)z * MN + i);
         float v[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float b = bias ? ld(bias, b_dt, bi + k) : 0.f;
             const float r = res ? ld(res, o_dt, ri + k) : 0.f;
-            v[k] = finish(acc[k] + b, r, epi, order, s);
+            v[k] = finish(acc[k], r, epi, order, s);
         }
         if (o_dt == DT_F16) {
             typedef half_t half4t __attribute__((ext_vector_type(4)));

@@ -76,10 +76,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p)
 
     // ---- scores: tiles the mask hides entirely are -inf without any MFMA ----
     if constexpr (EK == EpiKind::Scores) {
-        const int64_t last_q = (int64_t)m0 + BM - 1 + p.causal_offset;   // key limit of the tile's last query
-        const int64_t first_q = (int64_t)m0 + p.causal_offset;
-        const bool hidden = (p.causal && (int64_t)n0 > last_q) ||
-                            (p.span && (int64_t)n0 + BN - 1 < first_q + 1 - (int64_t)p.span);
+        // the tile's rows read at most keys [key_start(first row), key_end(last row))
+        const uint32_t last = (m0 + BM < M ? m0 + BM : M) - 1;
+        const bool hidden = (int64_t)n0 >= p.mask.key_end(last) || (int64_t)n0 + BN <= p.mask.key_start(m0);
         if (hidden) {
             float* C = (float*)p.C + bz * p.c_batch_stride;
             for (int i = tid; i < BM * BN; i += 256) {
@@ -277,9 +276,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p)
                             st(p.C, p.c_dtype, o, finish(v + b, rr, p.epilogue, p.residual_order, p.scalar_scale));
                         }
                     } else if constexpr (EK == EpiKind::Scores) {
-                        const int64_t pos = (int64_t)row + p.causal_offset;
-                        const bool hide = (p.causal && (int64_t)col > pos) ||
-                                          (p.span && pos >= (int64_t)p.span && (int64_t)col < pos + 1 - (int64_t)p.span);
+                        const bool hide = (int64_t)col >= p.mask.key_end(row) || (int64_t)col < p.mask.key_start(row);
                         ((float*)p.C)[bz * p.c_batch_stride + (size_t)row * N + col] =
                             hide ? -__builtin_inff() : v * p.scalar_scale;
                     } else {   // Conv: row = output channel, col = output position

@@ -39,6 +39,43 @@ enum class EpiKind : int {
     Conv = 3,      // per-row (channel) scale / bias, epilogue, residual
 };
 
+// The attention mask of /root/reference/vai/shaders/common/causal_mask.h:25-42
+// for the no-cache case: query t (0 <= t < tq) sits at key position
+// t + tkv - tq and reads keys [key_start(t), key_end(t)). The token end comes
+// from a list of blocks, each causal or not (the first block in the highest of
+// `blocks` bits, ends end[0..blocks-2] in query rows, the last block ends at
+// tq); 0 blocks is no mask. span > 0 keeps only the last span keys of each
+// query (a sliding window). Both bounds are non-decreasing in t, so a range
+// of rows [t0, t1) reads at most [key_start(t0), key_end(t1 - 1)).
+struct MaskRule {
+    uint32_t tq, tkv;
+    uint32_t blocks, bits;
+    uint32_t end[31];
+    uint32_t span;
+
+    __host__ __device__ uint32_t new_token_end(uint32_t t) const
+    {
+        if (blocks == 0) return tq;
+        uint32_t k = 0, e = tq;
+        for (; k + 1 < blocks; ++k) {
+            const uint32_t b = end[k] < tq ? end[k] : tq;
+            if (t < b) { e = b; break; }
+        }
+        return ((bits >> (blocks - 1 - k)) & 1u) ? t + 1 : e;
+    }
+    __host__ __device__ int64_t key_end(uint32_t t) const
+    {
+        const int64_t e = (int64_t)new_token_end(t) + tkv - tq;
+        return e < 0 ? 0 : (e > (int64_t)tkv ? (int64_t)tkv : e);
+    }
+    __host__ __device__ int64_t key_start(uint32_t t) const
+    {
+        const int64_t pos = (int64_t)t + tkv - tq;
+        const int64_t p = pos < 0 ? 0 : pos;
+        return (span == 0 || p < (int64_t)span) ? 0 : p + 1 - span;
+    }
+};
+
 struct GemmParams {
     // A [M, K] row-major (lda = K), B per BKind, C per EpiKind.
     const void* A;
@@ -65,6 +102,7 @@ struct GemmParams {
     // Scores
     uint32_t causal, span;
     int32_t causal_offset;        // Tkv - Tq
+    MaskRule mask;                // mask.blocks > 1: the block list rules (causal unused)
     // Conv: image geometry (B side is the gathered input)
     const void* conv_scale;
     uint32_t ci, hi, wi, wo, ks, stride;
@@ -86,6 +124,10 @@ size_t gemm_packed_weight_bytes(uint32_t N, uint32_t K, uint32_t H, bool gated);
 hipError_t gemm_pack_weight(void* dst, const void* w, uint32_t N, uint32_t K, uint32_t H, bool gated, hipStream_t s);
 hipError_t gemm_packed_launch(const GemmParams& p, const void* packed, bool gated, hipStream_t s);
 
+// Linear with fp16 accumulation in the reference's exact fma order (any shape;
+// vector ALU, not the matrix cores, which accumulate in fp32 only).
+hipError_t gemm_acc16_launch(const GemmParams& p, bool gated, hipStream_t s);
+
 // fp32 Linear for small problems: a 32 x 16*nf tile per workgroup over the
 // full K (the waves split K and sum through LDS), no split-K workspace.
 bool gemm_f32_ok(const GemmParams& p);
@@ -106,6 +148,7 @@ struct AttnParams {
     uint32_t batch, hq, hkv, tq, tkv, head_dim;
     float scale;
     uint32_t causal, span;
+    MaskRule mask;                // the same rule; blocks > 1 takes the general per-row bounds
     // Key-range split (0 units: each workgroup walks all of its keys and
     // writes O). Otherwise each query tile's keys are cut into chunks of
     // chunk_tiles 64-key tiles, `units` work units per head; partial O and

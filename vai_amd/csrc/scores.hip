@@ -66,9 +66,9 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParam
 
     // Tiles the mask hides entirely: -inf, 16 bytes per lane.
     {
-        const int64_t first_q = (int64_t)m0 + p.causal_offset, last_q = first_q + T - 1;
-        const bool hidden = (p.causal && (int64_t)n0 > last_q) ||
-                            (p.span && (int64_t)n0 + T - 1 < first_q + 1 - (int64_t)p.span);
+        // the tile's rows read at most keys [key_start(first row), key_end(last row))
+        const uint32_t last = (m0 + T < M ? m0 + T : M) - 1;
+        const bool hidden = (int64_t)n0 >= p.mask.key_end(last) || (int64_t)n0 + T <= p.mask.key_start(m0);
         if (hidden) {
             // each wave fills its (T/2)x(T/2) block, 16 bytes per lane and
             // 1 KB per store instruction; rows past M and columns past N are
@@ -169,7 +169,9 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParam
                           (p.span && (int64_t)n0 < q0 + T - (int64_t)p.span);
     const float scale = p.scalar_scale;
     const uint32_t rw0 = wm * HT + 4 * fk, cw0 = wn * HT + fr;     // this lane's row / column in the tile
-    if (m0 + T <= M && n0 + T <= N) {
+    // A block list (more than one block) takes the checked path below, which
+    // reads each row's key bounds from the rule.
+    if (m0 + T <= M && n0 + T <= N && p.mask.blocks <= 1) {
         const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(S + (size_t)m0 * N + n0), (short)0, 0x7FFFFFFF, 0x00020000);
         const uint32_t lane_off = (rw0 * N + cw0) * 4;
@@ -205,9 +207,7 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParam
                 constexpr int i = I, j = J, r = R;
                 const uint32_t row = m0 + rw0 + i * 32 + (r % 4) + 8 * (r / 4), col = n0 + cw0 + j * 32;
                 if (row < M && col < N) {
-                    const int64_t pos = (int64_t)row + p.causal_offset, c = col;
-                    const bool hide = (p.causal && c > pos) ||
-                                      (p.span && pos >= (int64_t)p.span && c < pos + 1 - (int64_t)p.span);
+                    const bool hide = (int64_t)col >= p.mask.key_end(row) || (int64_t)col < p.mask.key_start(row);
                     S[(size_t)row * N + col] = hide ? -__builtin_inff() : acc[i][j][r] * scale;
                 }
             });
@@ -239,7 +239,7 @@ static hipError_t scores_launch_t(const GemmParams& p, hipStream_t s)
 // scores keep 128x128 tiles (fewer Q/K re-reads, 12.8 against 13.2 us).
 hipError_t scores_launch(const GemmParams& p, hipStream_t s)
 {
-    return (p.causal || p.span) ? scores_launch_t<64>(p, s) : scores_launch_t<128>(p, s);
+    return (p.causal || p.span || p.mask.blocks > 1) ? scores_launch_t<64>(p, s) : scores_launch_t<128>(p, s);
 }
 
 }   // namespace vai_dev

@@ -22,6 +22,20 @@ static void check(vai_status st, const char* what)
 
 static void* ptrOrNull(const Tensor& t) { return t.validShape() ? t.devicePtr() : nullptr; }
 
+// causal / span from the node's config, or the block mask when one is set
+template <class Args>
+static void apply_mask(Args& a, bool causal, uint32_t span, const CausalMask& m)
+{
+    a.causal = causal ? 1 : 0;
+    a.span = span;
+    if (m.blockCount == 0) return;
+    a.causal = 0;
+    a.span = m.span;
+    a.mask_blocks = m.blockCount;
+    a.mask_bits = m.bits;
+    for (uint32_t k = 0; k + 1 < m.blockCount; ++k) a.mask_block_end[k] = m.blockEnd[k];
+}
+
 // ---------------------------------------------------------------- Linear ----
 
 Linear::Linear(Config config) : config_(config)
@@ -54,6 +68,7 @@ vai_linear_args Linear::args(bool withPointers) const
     a.residual_repeat = residualRepeat_;
     a.scalar_scale = config_.scalarScale;
     a.split_size = config_.splitSize;
+    a.acc_dtype = accDtype_ == Dtype::Fp16 ? VAI_DTYPE_F16 : VAI_DTYPE_F32;
     if (fused_) {
         a.gated = 1;
         a.gate_epilogue = uint32_t(fused_->config_.activation);
@@ -330,12 +345,23 @@ void AttentionScores::run(CommandStream& cmd)
     a.head_dim = config_.headDim;
     a.dtype = code((*this)["in0"].dtype());
     a.scale = config_.scale != 0.0f ? config_.scale : 1.0f / std::sqrt(float(config_.headDim));
-    a.causal = config_.causal ? 1 : 0;
-    a.span = config_.span;
+    apply_mask(a, config_.causal, config_.span, mask_);
     check(vai_attn_scores_launch(&a, (vai_stream_t)cmd.stream()), "AttentionScores");
 }
 
+void AttentionScores::setCausalMask(const CausalMask& mask)
+{
+    mask_ = mask;
+    if (ownedNet_) ownedNet_->invalidateCommandBuffer();
+}
+
 // ------------------------------------------------------------- Attention ----
+
+void Attention::setCausalMask(const CausalMask& mask)
+{
+    mask_ = mask;
+    if (ownedNet_) ownedNet_->invalidateCommandBuffer();
+}
 
 Attention::Attention(Config config) : config_(config)
 {
@@ -361,8 +387,7 @@ vai_attention_args Attention::args(bool withBuffers) const
     a.tkv = tkv_;
     a.head_dim = config_.headDim;
     a.scale = config_.scale;
-    a.causal = config_.causal ? 1 : 0;
-    a.span = config_.span;
+    apply_mask(a, config_.causal, config_.span, mask_);
     // the size query needs non-null operands; their values do not matter
     alignas(16) static char dummy[16];
     a.q = a.k = a.v = dummy;

@@ -8,6 +8,7 @@
 // Configs keep the reference's field names and defaults; prepare() validates
 // and picks the kernel through the C ABI, run() launches on the net's stream.
 #pragma once
+#include <array>
 #include <cstdint>
 
 #include "../../include/vai_amd.h"
@@ -51,9 +52,15 @@ public:
     const char* kind() const override { return "Linear"; }
 
     bool hasBias() const { return (*this)["bias"].validShape(); }
-    // The kernels accumulate in fp32 whatever is asked: fp32 is the reference's
-    // AMD default (linear.h:2320) and an fp16 request only narrows precision.
-    void setAccDtype(Dtype dtype, DtypeKey) { accDtype_ = dtype; }
+    // Accumulator dtype (linear.h:289,2320). None and Fp32 accumulate in fp32,
+    // the reference's AMD default; Fp16 sums in fp16 in the reference tile
+    // kernel's order wherever that kernel would (M > 8, an fp16 operand).
+    // A change after the first forward takes effect at the next one (re-record).
+    void setAccDtype(Dtype dtype, DtypeKey)
+    {
+        if (dtype != accDtype_ && ownedNet_) ownedNet_->invalidateCommandBuffer();
+        accDtype_ = dtype;
+    }
     Dtype accDtype() const { return accDtype_; }
 
     // The kernel prepare() chose ("slab", "tile_f16_256x256_gated", ...) and its split count.
@@ -125,6 +132,24 @@ private:
     uint32_t batch_ = 1, hi_ = 0, wi_ = 0;
 };
 
+// A block mask as the reference's writeCausalMask sets it (/root/reference/
+// vai/nodes/attention.h:40-55): blockEnd lists every block end but the last
+// (query rows, increasing, the list stops at its first 0), bit (count - 1 - k)
+// of bits marks block k causal, span > 0 is a sliding window.
+using CausalBlockEnd = std::array<uint32_t, VAI_MAX_CAUSAL_BLOCKS - 1>;
+struct CausalMask {
+    uint32_t blockCount = 0;   // 0: the node's causal flag alone
+    uint32_t bits = 0;
+    CausalBlockEnd blockEnd{};
+    uint32_t span = 0;
+    static CausalMask make(uint32_t bits, const CausalBlockEnd& blockEnd = {}, uint32_t span = 0)
+    {
+        CausalMask m{1, bits, blockEnd, span};
+        while (m.blockCount < VAI_MAX_CAUSAL_BLOCKS && blockEnd[m.blockCount - 1] != 0) ++m.blockCount;
+        return m;
+    }
+};
+
 class AttentionScores : public Node
 {
 public:
@@ -141,9 +166,12 @@ public:
     void prepare() override;
     void run(CommandStream& cmd) override;
     const char* kind() const override { return "AttentionScores"; }
+    // Replaces causal/span with the block mask; the next forward re-records.
+    void setCausalMask(const CausalMask& mask);
 
 private:
     uint32_t batch_ = 1, tq_ = 0, tkv_ = 0;
+    CausalMask mask_;
 };
 
 // The reference's Attention node without a KV cache (/root/reference/vai/
@@ -168,10 +196,15 @@ public:
     void prepare() override;
     void run(CommandStream& cmd) override;
     const char* kind() const override { return "Attention"; }
+    // The reference's setCausalMask role: replaces causal/span with the block
+    // mask. The reference rewrites a uniform buffer without re-recording; here
+    // the mask is part of the recorded launch, so the next forward re-records.
+    void setCausalMask(const CausalMask& mask);
 
 private:
     vai_attention_args args(bool withBuffers) const;
     uint32_t batch_ = 1, tq_ = 0, tkv_ = 0;
+    CausalMask mask_;
 };
 
 }   // namespace node

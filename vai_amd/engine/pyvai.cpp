@@ -84,6 +84,14 @@ public:
 
 }   // namespace
 
+static vai::node::CausalBlockEnd block_ends(const std::vector<uint32_t>& ends)
+{
+    vai::node::CausalBlockEnd e{};
+    if (ends.size() > e.size()) throw std::invalid_argument("at most 31 block ends");
+    std::copy(ends.begin(), ends.end(), e.begin());
+    return e;
+}
+
 PYBIND11_MODULE(_pyvai, m)
 {
     m.doc() = "vai_amd engine: NeuralNet / Tensor / nodes on MI355X kernels";
@@ -137,6 +145,7 @@ PYBIND11_MODULE(_pyvai, m)
         .def_property_readonly("record_count", &PyNet::recordCount)
         .def_property_readonly("submit_count", &PyNet::submitCount)
         .def("set_o_dtype", [](PyNet& net, Node& n, Dtype d) { n.setODtype(d, net.key()); })
+        .def("set_acc_dtype", [](PyNet& net, node::Linear& l, Dtype d) { l.setAccDtype(d, net.key()); })
         .def("__call__", [](PyNet& net, py::kwargs kw) {
             TensorDict in;
             for (auto item : kw) in[item.first.cast<std::string>()] = item.second.cast<Tensor>();
@@ -194,7 +203,10 @@ PYBIND11_MODULE(_pyvai, m)
                  return std::make_unique<node::AttentionScores>(c);
              }),
              py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0, py::arg("causal") = true,
-             py::arg("span") = 0, py::arg("scale") = 0.0f);
+             py::arg("span") = 0, py::arg("scale") = 0.0f)
+        .def("set_causal_mask", [](node::AttentionScores& n, uint32_t bits, std::vector<uint32_t> ends, uint32_t span) {
+                 n.setCausalMask(node::CausalMask::make(bits, block_ends(ends), span));
+             }, py::arg("bits"), py::arg("block_end") = std::vector<uint32_t>{}, py::arg("span") = 0);
     py::class_<node::Attention, Node>(nodes, "AttentionNode")
         .def(py::init([](uint32_t num_q_heads, uint32_t head_dim, uint32_t num_kv_heads, bool causal, uint32_t span,
                          float scale) {
@@ -203,5 +215,8 @@ PYBIND11_MODULE(_pyvai, m)
                  return std::make_unique<node::Attention>(c);
              }),
              py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0, py::arg("causal") = true,
-             py::arg("span") = 0, py::arg("scale") = 0.0f);
+             py::arg("span") = 0, py::arg("scale") = 0.0f)
+        .def("set_causal_mask", [](node::Attention& n, uint32_t bits, std::vector<uint32_t> ends, uint32_t span) {
+                 n.setCausalMask(node::CausalMask::make(bits, block_ends(ends), span));
+             }, py::arg("bits"), py::arg("block_end") = std::vector<uint32_t>{}, py::arg("span") = 0);
 }

@@ -130,7 +130,8 @@ def build_cases(capi, stream, which):
         ws = [D(w0) for _ in range(copies)]
         for m in (1, 4, 8):
             x = D(f16(np.random.default_rng(m).standard_normal((m, 2048))))
-            fn, kern = linear_case(x, ws)
+            # each W copy packed once, as the engine's Linear does at prepare (M >= 3 reads it)
+            fn, kern = linear_case(x, ws, pack=True)
             byts = 2048 * 8192 * 2 + m * 2048 * 2 + m * 8192 * 4
             cases[f"2/M={m}"] = Case(f"decode GEMV M={m} K=2048 N=8192 fp16 W, fp32 acc/out", "GB/s",
                                      byts / 1e9, "hbm", HBM_PEAK_GBS, fn, kern, 2 * m * 2048 * 8192, byts, "f16", f"2/M={m}")
@@ -256,7 +257,45 @@ def build_cases(capi, stream, which):
         cases[key] = Case(f"YOLOX-s {ks}x{ks}/s{st} conv in[1,{ci},{hw},{hw}] W[{co},{ci},{ks},{ks}] fp16 +bias SiLU, fp32 out",
                           "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnc, f"conv_kernel<{ks}> (implicit GEMM, packed weight)",
                           flops, byts, "f16", key)
+    if "read" in which or "empty" in which:
+        # the ceiling for config 2: a plain read of W's 32 MiB, rotated like the
+        # GEMV's W copies (vai_amd/probe/read_ceiling.hip), and an empty launch
+        probe = ctypes.CDLL(os.path.join(ROOT, "vai_amd", "libvai_probe.so"))
+        probe.vai_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+        probe.vai_probe_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        sink = capi.DeviceArray((1,), np.float32)
+        nbytes = 2048 * 8192 * 2
+        bufs = [capi.DeviceArray((nbytes,), np.uint8) for _ in range(max(2, ROTATE_BYTES // nbytes))]
+        for b in bufs:
+            b.fill_(0)
+        variants = [(v, g, t, l) for v, (g, t, l) in READ_VARIANTS.items()] if "read" in which else []
+        for name, g, t, l in variants:
+            def fnr(i, g=g, t=t, l=l):
+                capi.check(probe.vai_probe_read(bufs[i % len(bufs)].ptr, nbytes, g, t, l, sink.ptr, stream.ptr), "read")
+            fnr.keep = [bufs, sink, probe]
+            cases[f"read/{name}"] = Case(f"plain read of 32 MiB ({g} workgroups x {t} threads, {l} x 16 B loads per lane "
+                                         f"in flight), rotating {len(bufs)} buffers", "GB/s", nbytes / 1e9, "hbm",
+                                         HBM_PEAK_GBS, fnr, "read_kernel (vai_amd/probe)", 0, nbytes, "f16", "read")
+        if "empty" in which:
+            for g in (1, 256, 1024):
+                def fne(i, g=g):
+                    capi.check(probe.vai_probe_empty(g, 256, sink.ptr, stream.ptr), "empty")
+                fne.keep = [sink, probe]
+                cases[f"empty/{g}"] = Case(f"empty kernel, {g} workgroups of 256", "us", 0.0, "hbm", HBM_PEAK_GBS, fne,
+                                           "empty_kernel (vai_amd/probe)", 0, 0, "-", "empty")
     return cases
+
+
+# plain-read variants: name -> (workgroups, threads per workgroup, loads per lane)
+READ_VARIANTS = {
+    "gemv_shape": (1024, 256, 8),      # the M=1 GEMV's grid: 4096 waves of 8 KB
+    "wg512": (512, 512, 8),
+    "wg1024x256thr": (256, 1024, 8),
+    "16loads": (512, 256, 16),
+    "32loads": (256, 256, 32),
+    "4loads": (2048, 256, 4),
+}
 
 
 def time_case(capi, stream, case, steps, warmup, repeats):
@@ -407,6 +446,11 @@ def main():
     report = {}
     for key, case in cases.items():
         ms = time_case(capi, stream, case, args.steps, args.warmup, args.repeats)
+        if case.unit == "us":   # empty-launch probe: the per-step time is the figure
+            report[key] = {"workload": case.name, "kernel": case.kernel, "value": round(ms * 1e3, 3), "unit": "us",
+                           "ms_per_step": round(ms, 6), "dtype": case.dtype}
+            print(f"# {key}: {case.name}: {ms*1e3:.2f} us/step", file=sys.stderr, flush=True)
+            continue
         rate = case.work / (ms * 1e-3)
         achieved = (case.bytes / 1e9 if case.bound == "hbm" else case.flops / 1e12) / (ms * 1e-3)
         report[key] = {
@@ -419,7 +463,8 @@ def main():
         print(f"# cfg {key}: {case.name}: {ms*1e3:.2f} us/step, {rate:.1f} {case.unit}, "
               f"{100*achieved/case.peak:.1f}% of {case.bound} peak [{case.kernel}]", file=sys.stderr, flush=True)
     if not args.no_cpu:
-        for key, cb in cpu_baseline(list(report), args.cpu_seconds).items():
+        for key, cb in cpu_baseline([k for k in report if not k.startswith(("read", "empty"))],
+                                    args.cpu_seconds).items():
             report[key]["cpu_baseline"] = cb
     prim = report.get("2/M=1") or next(iter(report.values()))
     line = {

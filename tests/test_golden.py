@@ -157,6 +157,24 @@ def test_gpu_cfg2(gpu, m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_gpu_cfg2_packed(gpu, m):
+    """Config 2 as bench.py times it: the weight packed once (vai_linear_pack_weight);
+    M >= 3 then runs the packed GEMV, M = 1 keeps the row-streaming kernel."""
+    x, w = C.cfg2()
+    D = gpu.DeviceArray.from_numpy
+    dx, dw = D(x[:m]), D(w)
+    out = gpu.DeviceArray((m, 8192), np.float32)
+    a = gpu.linear_args(out, dx, dw)
+    packed = gpu.linear_pack_weight(a)
+    a.packed_weight = packed.ptr
+    assert gpu.linear_plan(a)[0] == ("slab_packed" if m >= 3 else "slab")
+    got = gpu.linear(out, dx, dw, packed=packed).numpy()
+    assert_close(got, G["cfg2_out"][:m], FP32)
+    _mre(got, G["cfg2_out"][:m], _dot_mag(x[:m], w), MRE_F16, f"cfg2 packed M={m}")
+
+
+@pytest.mark.gpu
 def test_gpu_cfg3(gpu):
     x, w = C.cfg3()
     D = gpu.DeviceArray.from_numpy

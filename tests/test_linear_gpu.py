@@ -370,3 +370,56 @@ def test_linear_packed_repeatable(gpu, m, k, n, gated, odt):
     for _ in range(5):
         out.fill_(0xFF)
         np.testing.assert_array_equal(gpu.linear(out, dx, dw, db, packed=packed, **kw).numpy(), first)
+
+
+@pytest.mark.parametrize("m, k, n, epi, bias, resid, odt, gated", [
+    (3, 256, 1000, "NONE", True, False, np.float32, False),       # N tail inside a 32-row block
+    (4, 2048, 8192, "NONE", False, False, np.float32, False),     # config 2's shape
+    (8, 2048, 8192, "GELU_TANH", True, True, np.float32, False),
+    (5, 4096, 640, "SILU", True, False, np.float16, False),       # two fragment passes per wave
+    (8, 384, 96, "NONE", False, False, np.float32, False),        # fewer fragments than waves
+    (4, 512, 2 * 520, "SILU", True, False, np.float32, True),     # gated: packed gate/up blocks, H tail
+    (7, 1024, 2 * 4096, "GELU", False, False, np.float16, True),
+])
+def test_gemv_packed(gpu, m, k, n, epi, bias, resid, odt, gated):
+    """The decode GEMV over the packed weight (M 3-8) vs the oracle and vs the
+    row-streaming kernels on the same inputs."""
+    rng = np.random.default_rng(m * 100 + k)
+    w = draw(normal((n, k), 0.02), rng, np.float16)
+    b = draw(normal((n,), 0.02), rng, np.float16) if bias else None
+    x = draw((m, k), rng, np.float16)
+    cols = n // 2 if gated else n
+    r = draw((m, cols), rng, odt) if resid else None
+    kw = dict(gated=True, gate_epi=epi) if gated else dict(epi=epi)
+    D = gpu.DeviceArray.from_numpy
+    dx, dw = D(x), D(w)
+    db, dr = (D(b) if bias else None), (D(r) if resid else None)
+    out = gpu.DeviceArray((m, cols), odt)
+    a = gpu.linear_args(out, dx, dw, db, dr, **kw)
+    packed = gpu.linear_pack_weight(a)
+    a.packed_weight = packed.ptr
+    assert gpu.linear_plan(a)[0].startswith("slab_packed")
+    print(f"gemv packed m={m} k={k} n={n} gated={gated}", flush=True)
+    got = gpu.linear(out, dx, dw, db, dr, packed=packed, **kw).numpy()
+    if gated:
+        want = oracle.gated_mul(oracle.linear(x, w, b, stage="slab"), epi=epi, out_dtype=odt)
+    else:
+        want = oracle.linear(x, w, b, r, epi=epi, out_dtype=odt, stage="slab")
+    tol = FP16 if odt == np.float16 else (TRANS if epi != "NONE" else FP32)
+    assert_close(got.astype(np.float32), want.astype(np.float32), tol)
+    ref = run_linear(gpu, x, w, b, r, out_dtype=odt, **kw)
+    assert_close(got.astype(np.float32), ref.astype(np.float32), tol)
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_gemv_fp16_subnormals(gpu, m):
+    """fp16 weights and inputs with subnormal values (a device-made fp16
+    tensor keeps them): the GEMV's dot products must use them as stored."""
+    rng = np.random.default_rng(m)
+    k, n = 512, 256
+    w = (rng.standard_normal((n, k)) * 2.0 ** -16).astype(np.float16)   # mostly subnormal halves
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    assert (np.abs(w) < np.float16(2.0 ** -14)).mean() > 0.5
+    got = run_linear(gpu, x, w)
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    assert_close(got, want, (1e-5, 1e-9))

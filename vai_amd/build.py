@@ -108,9 +108,25 @@ def build(jobs=None, only_stale=False):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
     os.replace(tmp, LIB)
+    _build_probe()
     _build_pymodule()
     _build_cpp_programs()
     return LIB
+
+
+PROBE_SRC = os.path.join(HERE, "probe", "read_ceiling.hip")
+PROBE_LIB = os.path.join(HERE, "libvai_probe.so")
+
+
+def _build_probe():
+    """libvai_probe.so: bench.py's measurement kernels (the plain-read ceiling),
+    kept out of the product library."""
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [HIPCC] + COMMON + DEVICE_FLAGS + ["-shared", PROBE_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("probe build failed:\n" + r.stderr)
+    os.replace(tmp, PROBE_LIB)
 
 
 def _build_cpp_programs():

@@ -29,6 +29,7 @@ vai_status hip_status(hipError_t e) { return e == hipSuccess ? VAI_OK : (vai_sta
 
 struct LinearPlan {
     enum Kind { Slab, SlabThenGate, Tile, BigTile, PackedTile, F32Small, Acc16Tile } kind;
+    bool packed_gemv;   // Slab / SlabThenGate over the packed weight
     GemmTile tile;
     uint32_t bm, bn;
     uint32_t split_size, splits;
@@ -62,12 +63,24 @@ vai_status check_linear(const vai_linear_args* a)
     return VAI_OK;
 }
 
+// The packed weight's shapes: fp16 I and W, K % 128 == 0, K >= 256.
+bool linear_packable(const vai_linear_args* a)
+{
+    return a && a->i_dtype == VAI_DTYPE_F16 && a->w_dtype == VAI_DTYPE_F16 && a->N > 0 && a->K >= 256 &&
+           a->K % 128 == 0 && (!a->gated || a->N % 2 == 0);
+}
+
 LinearPlan plan_linear(const vai_linear_args* a)
 {
     LinearPlan p{};
     const uint32_t M = a->M, N = a->N, K = a->K;
     if (M <= 8) {
         p.kind = a->gated ? LinearPlan::SlabThenGate : LinearPlan::Slab;
+        // From 3 rows on, the matrix cores over the packed weight (whole 1 KB
+        // fragments per load) beat the VALU dot products; 1-2 rows stream W
+        // rows directly (measured on config 2: 6.4 vs 7.2 us at M = 1).
+        p.packed_gemv = a->packed_weight && M >= 3 && linear_packable(a) &&
+                        ((uintptr_t)a->packed_weight % 16) == 0 && ((uintptr_t)a->in % 16) == 0;
         p.splits = 1;
         p.split_size = K;
         p.workspace = a->gated ? (size_t)M * N * 4 : 0;
@@ -198,7 +211,10 @@ vai_status vai_linear_plan(const vai_linear_args* a, char* name, size_t name_len
         SlabParams sp{};
         sp.K = a->K; sp.w_dtype = a->w_dtype; sp.i_dtype = a->i_dtype; sp.weight = a->weight; sp.in = a->in;
         sp.M = a->M;
-        snprintf(buf, sizeof buf, "%s%s", (sp.M >= 2 && gemv_mfma_ok(sp)) ? "slab_mfma" : slab_vec_ok(sp) ? "slab" : "slab_scalar",
+        snprintf(buf, sizeof buf, "%s%s",
+                 p.packed_gemv ? "slab_packed"
+                 : (sp.M >= 5 && gemv_mfma_ok(sp)) ? "slab_mfma"
+                 : slab_vec_ok(sp) ? "slab" : "slab_scalar",
                  p.kind == LinearPlan::SlabThenGate ? "+gate" : "");
     } else if (p.kind == LinearPlan::Acc16Tile) {
         snprintf(buf, sizeof buf, "tile_acc16_64x64%s", a->gated ? "_gated" : "");
@@ -232,11 +248,13 @@ static vai_status linear_run(const vai_linear_args* a, const LinearPlan& p, hipS
         sp.scalar_scale = a->scalar_scale;
         if (p.kind == LinearPlan::Slab) {
             sp.out = a->out; sp.o_dtype = a->o_dtype;
+            if (p.packed_gemv) return hip_status(gemv_packed_launch(sp, a->packed_weight, false, nullptr, s));
             return hip_status(slab_launch(sp, s));
         }
         // Gated at M <= 8: the fp32 Linear output, then the gating pass.
         sp.out = a->workspace; sp.o_dtype = VAI_DTYPE_F32;
-        hipError_t e = slab_launch(sp, s);
+        hipError_t e = p.packed_gemv ? gemv_packed_launch(sp, a->packed_weight, true, (float*)a->workspace, s)
+                                     : slab_launch(sp, s);
         if (e != hipSuccess) return hip_status(e);
         return hip_status(gated_mul_launch(a->out, a->o_dtype, a->workspace, VAI_DTYPE_F32, a->M, a->N / 2,
                                            a->gate_epilogue, s));
@@ -329,15 +347,6 @@ vai_status vai_linear_launch_noalloc(const vai_linear_args* a, vai_stream_t stre
         b.workspace_bytes = VAI_NOALLOC_SCRATCH_BYTES;
     }
     return linear_run(&b, p, (hipStream_t)stream);
-}
-
-// The packed path needs fp16 I and W and K % 128 == 0, K >= 256 (two K
-// stages per loop trip, copies at most one tile ahead); the size does not
-// depend on M.
-static bool linear_packable(const vai_linear_args* a)
-{
-    return a && a->i_dtype == VAI_DTYPE_F16 && a->w_dtype == VAI_DTYPE_F16 && a->N > 0 && a->K >= 256 &&
-           a->K % 128 == 0 && (!a->gated || a->N % 2 == 0);
 }
 
 size_t vai_linear_packed_weight_size(const vai_linear_args* a)

@@ -105,6 +105,89 @@ hipError_t gemm_pack_weight(void* dst, const void* w, uint32_t N, uint32_t K, ui
     return hipGetLastError();
 }
 
+// ---- decode GEMV over the packed weight (M <= 8) ----------------------------
+// In the packed layout one 32x32x16 MFMA B fragment (32 rows x 16 k) is 1 KB
+// of contiguous memory, so the GEMV reads W in whole 1 KB pieces per load
+// instruction and the matrix cores take the products: X is the A operand
+// (rows >= M read as zero), each output row of W a column. A workgroup of 16
+// waves owns one 32-row block; its K/16 fragments are split over the waves,
+// each issuing all of its (up to 8) fragment loads before the X loads and the
+// MFMAs, and the 16 partial 8x32 results meet in LDS. (Loading the MFMA layout
+// from an unpacked W reads 16 rows x 64 B per instruction and measured about
+// 1 us slower per 32 MiB; staging unpacked rows through LDS, 1.5-2 us.)
+constexpr int GV_WAVES = 16, GV_FR = 8;
+
+// EXACT: K/16 is a multiple of GV_WAVES * GV_FR, so every wave runs whole
+// passes of GV_FR fragments with no guards (straight-line loads, per-fragment
+// waits). Rows past M read X row 0 (a valid address); their results are
+// never stored. A padding block (no row of W) skips its passes but still
+// meets the barrier: no branch ahead of the loads, so the compiler fetches
+// the kernel arguments in one batch.
+template <bool EXACT>
+__global__ __launch_bounds__(1024) void gemv_packed_kernel(SlabParams a, const half8* __restrict__ packed,
+                                                           uint32_t H, int gated, float* __restrict__ ygated)
+{
+    __shared__ float part[GV_WAVES][8][33];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lb = blockIdx.x, K = a.K, M = a.M, N = a.N;
+    // the arguments the loads need, fetched in one batch at entry (the
+    // compiler otherwise fetches each behind the branch that first uses it)
+    asm volatile("" ::"s"(packed), "s"(a.in), "s"(K), "s"(M), "s"(N), "s"(H), "s"(gated));
+    const bool live = packed_src_row(lb, 0, gated != 0, H, N) != 0xFFFFFFFFu;   // uniform
+    const uint32_t frags = K / 16, per = (frags + GV_WAVES - 1) / GV_WAVES;
+    const uint32_t f0 = wave * per, f1 = live ? std::min(frags, f0 + per) : f0;
+    const half8* wp = packed + (size_t)lb * frags * 64 + lane;   // fragment f at wp + 64 f
+    const int xm = lane & 31, xg = lane >> 5;
+    const half_t* xp = (const half_t*)a.in + (size_t)((uint32_t)xm < M ? xm : 0) * K + xg * 8;
+    float16v acc0 = (float16v)0.f, acc1 = (float16v)0.f;
+    for (uint32_t fb = f0; fb < f1; fb += GV_FR) {
+        half8 wv[GV_FR], xv[GV_FR];
+#pragma unroll
+        for (int i = 0; i < GV_FR; ++i) {
+            wv[i] = (EXACT || fb + i < f1) ? __builtin_nontemporal_load(wp + (size_t)(fb + i) * 64) : (half8)0;
+            xv[i] = (EXACT || fb + i < f1) ? *(const half8*)(xp + (size_t)(fb + i) * 16) : (half8)0;
+        }
+        // every load of the pass in flight before the first MFMA (left alone,
+        // the scheduler trades that for registers: load, wait, MFMA, ...)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < GV_FR; i += 2) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xv[i], wv[i], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(xv[i + 1], wv[i + 1], acc1, 0, 0, 0);
+        }
+    }
+    // rows 0..7 of the 32x32 result: register rr < 4 holds row rr + 4 (lane / 32), column lane % 32
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) part[wave][rr + 4 * xg][xm] = acc0[rr] + acc1[rr];
+    __syncthreads();
+    if (threadIdx.x >= 8 * 32) return;
+    const uint32_t m = threadIdx.x / 32, n = threadIdx.x % 32;
+    const uint32_t row = packed_src_row(lb, n, gated != 0, H, N);
+    if (m >= M || row == 0xFFFFFFFFu) return;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < GV_WAVES; ++w) v += part[w][m][n];
+    const size_t o = (size_t)m * N + row;
+    if (gated) {   // the Linear output with its bias; the gating pass reads it
+        ygated[o] = v + (a.bias ? ld(a.bias, a.b_dtype, a.bias_repeat ? o % a.bias_repeat : o) : 0.f);
+        return;
+    }
+    store_output(OutputSpec{a.out, a.bias, a.residual, a.o_dtype, a.b_dtype, a.bias_repeat, a.residual_repeat,
+                            a.epilogue, a.residual_order, a.scalar_scale},
+                 o, v);
+}
+
+hipError_t gemv_packed_launch(const SlabParams& a, const void* packed, bool gated, float* ygated, hipStream_t s)
+{
+    const uint32_t H = gated ? a.N / 2 : 0;
+    const uint32_t blocks = packed_blocks(a.N, H, gated);
+    auto kern = (a.K / 16) % (GV_WAVES * GV_FR) == 0 ? gemv_packed_kernel<true> : gemv_packed_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * GV_WAVES), 0, s, a, (const half8*)packed, H, gated ? 1 : 0,
+                       ygated);
+    return hipGetLastError();
+}
+
 // Keeps a substep's MFMA operands allocated until all of its MFMAs have
 // issued: the fragment loads interleaved with those MFMAs then cannot be
 // given a register an issued-but-not-started MFMA still has to read.

@@ -23,6 +23,11 @@ struct SlabParams {
 bool slab_vec_ok(const SlabParams& a);
 bool gemv_mfma_ok(const SlabParams& a);
 hipError_t slab_launch(const SlabParams& a, hipStream_t s);
+// fp16 I and W, M <= 8, over the packed weight of gemm_pack_weight (same
+// layout as the prefill path). Gated: writes the raw [M, 2H] Linear output to
+// ygated in the original row order (the gating pass follows); otherwise O with
+// the full epilogue.
+hipError_t gemv_packed_launch(const SlabParams& a, const void* packed, bool gated, float* ygated, hipStream_t s);
 
 // The operand a GEMM's "B" side reads: C[M,N] = A[M,K] . B[N,K]^T.
 enum class BKind : int {

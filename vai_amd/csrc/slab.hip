@@ -17,10 +17,17 @@
 #include "launch_once.h"
 
 #include <algorithm>
+#include <type_traits>
 
 #define LDS_AS __attribute__((address_space(3)))
 
 namespace vai_dev {
+
+__device__ __forceinline__ OutputSpec slab_output(const SlabParams& a)
+{
+    return OutputSpec{a.out, a.bias, a.residual, a.o_dtype, a.b_dtype, a.bias_repeat, a.residual_repeat,
+                      a.epilogue, a.residual_order, a.scalar_scale};
+}
 
 template <typename T> struct Vec16;
 template <> struct Vec16<half_t> { typedef half8 type; static constexpr int n = 8; };
@@ -97,6 +104,110 @@ constexpr int butterfly_low()
     return low;
 }
 
+// The dot products of one 16-byte W chunk against one X chunk: v_dot2_f32_f16
+// for fp16 x fp16 (two exact products into the fp32 sum per instruction, half
+// the VALU work of widening each operand), fp32 FMAs otherwise.
+template <typename TI, typename TW, typename WV, typename XV>
+__device__ __forceinline__ float chunk_dot(const WV& w, const XV& x, float s)
+{
+    constexpr int EPC = Vec16<TW>::n;
+    if constexpr (std::is_same_v<TI, half_t> && std::is_same_v<TW, half_t>) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int e = 0; e < EPC; e += 2) s = __builtin_amdgcn_fdot2(h2{w[e], w[e + 1]}, h2{x[e], x[e + 1]}, s, false);
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) s = fmaf((float)w[e], (float)x[e], s);
+    }
+    return s;
+}
+
+// Few input rows (MP <= 2, or <= 4 when fp16): each lane keeps its X chunks in
+// registers. Per K block the wave issues every W load of its R rows, then the
+// X loads (L2-resident; issued before W, every wave's X fetch delayed the
+// whole W stream), then computes as the loads land. A wave whose rows and
+// block lie inside W runs a straight-line block with no per-load guards
+// (exec-mask branches around each load spread the issue over hundreds of
+// cycles and made the compiler wait for every load before the first product).
+// ALL_FULL (N a multiple of 4R, K of the block): no guards anywhere, so the
+// compiler interleaves each chunk's W and X loads and starts each chunk's
+// products as it lands (config 2 at M = 1: 6.4 us against 6.8 us with the
+// guarded block merged in).
+template <int MP, int R, int KCH, typename TI, typename TW, bool ALL_FULL>
+__global__ __launch_bounds__(256) void slab_reg_kernel(SlabParams a)
+{
+    typedef typename Vec16<TW>::type wvec;
+    constexpr int EPC = Vec16<TW>::n;      // W elements per 16-byte chunk
+    constexpr int KB = 64 * KCH * EPC;     // K elements per block iteration
+    constexpr int V = MP * R;              // dot products per lane
+    static_assert(V <= 64 && (V & (V - 1)) == 0, "butterfly needs a power of two <= 64");
+    typedef TI xvec __attribute__((ext_vector_type(EPC)));
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n0 = (blockIdx.x * 4u + wave) * R;
+    const uint32_t K = a.K, N = a.N, M = a.M;
+    const TW* __restrict__ W = (const TW*)a.weight;
+    const TI* __restrict__ X = (const TI*)a.in;
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+
+    auto block = [&](uint32_t kb, auto full_c) __attribute__((always_inline)) {
+        constexpr bool FULL = decltype(full_c)::value;
+        wvec wv[R][KCH];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int c = 0; c < KCH; ++c) {
+                const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
+                if (FULL || (n0 + r < N && k < K))
+                    wv[r][c] = __builtin_nontemporal_load((const wvec*)(W + (size_t)(n0 + r) * K + k));
+                else
+                    wv[r][c] = (wvec)0;
+            }
+        // rows past M read row 0 (a valid address); their sums are never stored
+        xvec xr[KCH][MP];
+#pragma unroll
+        for (int c = 0; c < KCH; ++c) {
+            const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
+#pragma unroll
+            for (int m = 0; m < MP; ++m) {
+                const uint32_t mr = (uint32_t)m < M ? (uint32_t)m : 0u;
+                xr[c][m] = (FULL || k < K) ? *(const xvec*)(X + (size_t)mr * K + k) : (xvec)0;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < KCH; ++c)
+#pragma unroll
+            for (int m = 0; m < MP; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[m * R + r] = chunk_dot<TI, TW>(wv[r][c], xr[c][m], acc[m * R + r]);
+    };
+    // K > 0 (the C ABI checks it): a loop that runs at least once lets the
+    // compiler fetch every kernel argument in one batch at entry (a `K > 0`
+    // test first had it fetch the weight pointer in a second, dependent round).
+    uint32_t kb = 0;
+    do {
+        if constexpr (ALL_FULL) block(kb, std::true_type{});
+        else if (n0 + R <= N && kb + KB <= K) block(kb, std::true_type{});
+        else block(kb, std::false_type{});
+        kb += KB;
+    } while (kb < K);
+
+    // Butterfly over the wave; afterwards lane `lane` holds value idx.
+    butterfly<V, 32>(acc, lane);
+    const int idx = butterfly_index<V>(lane);
+    if ((lane & (butterfly_low<V>() - 1)) != 0) return;
+    const uint32_t m = idx / R, r = idx % R;
+    if (m >= M || n0 + r >= N) return;
+    store_output(slab_output(a), (size_t)m * N + n0 + r, acc[0]);
+}
+
+
+// More input rows (5-8, or 3-8 with fp32 input): the M rows of each K block
+// are staged once per workgroup in LDS and broadcast to the four waves.
 template <int MP, int R, int KCH, typename TI, typename TW>
 __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
 {
@@ -105,10 +216,10 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
     constexpr int KB = 64 * KCH * EPC;     // K elements per block iteration
     constexpr int V = MP * R;              // dot products per lane
     static_assert(V <= 64 && (V & (V - 1)) == 0, "butterfly needs a power of two <= 64");
-    __shared__ TI xs[MP <= 2 ? 1 : MP * KB];
+    __shared__ TI xs[MP * KB];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n0 = (blockIdx.x * 4u + wave) * R;
     const uint32_t K = a.K, N = a.N, M = a.M;
     const TW* __restrict__ W = (const TW*)a.weight;
@@ -119,20 +230,6 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
 
     for (uint32_t kb = 0; kb < K; kb += KB) {
-        // 0. Few input rows: this lane's X chunks (L2-resident) first, so that
-        //    loads return in order X, then W chunk by chunk, and each chunk's
-        //    products start as soon as that chunk lands.
-        typedef TI xvec __attribute__((ext_vector_type(EPC)));
-        xvec xr[MP <= 2 ? KCH : 1][MP <= 2 ? MP : 1];
-        if constexpr (MP <= 2) {
-#pragma unroll
-            for (int c = 0; c < KCH; ++c) {
-                const uint32_t k = kb + (uint32_t)(c * 64 + lane) * EPC;
-#pragma unroll
-                for (int m = 0; m < MP; ++m)
-                    xr[c][m] = ((uint32_t)m < M && k < K) ? *(const xvec*)(X + (size_t)m * K + k) : (xvec)0;
-            }
-        }
         // 1. Every W load of this block for this wave's R rows, issued up front.
         wvec wv[R][KCH];
 #pragma unroll
@@ -145,50 +242,31 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
                 else
                     wv[r][c] = (wvec)0;
             }
-        if constexpr (MP <= 2) {
-            // 2'. Few input rows: the X chunks loaded in step 0, in registers;
-            //     no LDS, no barrier.
+        // 2. The M input rows of this block into LDS (zero past K and past M).
+        __syncthreads();
+        for (uint32_t i = threadIdx.x * EPC; i < (uint32_t)(MP * KB); i += 256 * EPC) {
+            const uint32_t m = i / KB, kk = kb + (i % KB);
+            // EPC elements of X per thread: K % EPC == 0 keeps them in one row.
+            typedef TI xvec __attribute__((ext_vector_type(EPC)));
+            xvec v = (m < M && kk < K) ? *(const xvec*)(X + (size_t)m * K + kk) : (xvec)0;
+            *(xvec*)(xs + i) = v;
+        }
+        __syncthreads();
+        // 3. Dot products.
 #pragma unroll
-            for (int c = 0; c < KCH; ++c) {
+        for (int c = 0; c < KCH; ++c) {
 #pragma unroll
-                for (int m = 0; m < MP; ++m) {
-                    const xvec xv = xr[c][m];
+            for (int m = 0; m < MP; ++m) {
+                float xf[EPC];
+                const TI* xp = xs + m * KB + (c * 64 + lane) * EPC;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float s = acc[m * R + r];
+                for (int e = 0; e < EPC; ++e) xf[e] = (float)xp[e];
 #pragma unroll
-                        for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], (float)xv[e], s);
-                        acc[m * R + r] = s;
-                    }
-                }
-            }
-        } else {
-            // 2. The M input rows of this block into LDS (zero past K and past M).
-            __syncthreads();
-            for (uint32_t i = threadIdx.x * EPC; i < (uint32_t)(MP * KB); i += 256 * EPC) {
-                const uint32_t m = i / KB, kk = kb + (i % KB);
-                // EPC elements of X per thread: K % EPC == 0 keeps them in one row.
-                typedef TI xvec __attribute__((ext_vector_type(EPC)));
-                xvec v = (m < M && kk < K) ? *(const xvec*)(X + (size_t)m * K + kk) : (xvec)0;
-                *(xvec*)(xs + i) = v;
-            }
-            __syncthreads();
-            // 3. Dot products.
+                for (int r = 0; r < R; ++r) {
+                    float s = acc[m * R + r];
 #pragma unroll
-            for (int c = 0; c < KCH; ++c) {
-#pragma unroll
-                for (int m = 0; m < MP; ++m) {
-                    float xf[EPC];
-                    const TI* xp = xs + m * KB + (c * 64 + lane) * EPC;
-#pragma unroll
-                    for (int e = 0; e < EPC; ++e) xf[e] = (float)xp[e];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float s = acc[m * R + r];
-#pragma unroll
-                        for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], xf[e], s);
-                        acc[m * R + r] = s;
-                    }
+                    for (int e = 0; e < EPC; ++e) s = fmaf((float)wv[r][c][e], xf[e], s);
+                    acc[m * R + r] = s;
                 }
             }
         }
@@ -200,10 +278,7 @@ __global__ __launch_bounds__(256) void slab_vec_kernel(SlabParams a)
     if ((lane & (butterfly_low<V>() - 1)) != 0) return;
     const uint32_t m = idx / R, r = idx % R;
     if (m >= M || n0 + r >= N) return;
-    const size_t o = (size_t)m * N + n0 + r;
-    const float b = a.bias ? ld(a.bias, a.b_dtype, a.bias_repeat ? o % a.bias_repeat : o) : 0.f;
-    const float rr = a.residual ? ld(a.residual, a.o_dtype, a.residual_repeat ? o % a.residual_repeat : o) : 0.f;
-    st(a.out, a.o_dtype, o, finish(acc[0] + b, rr, a.epilogue, a.residual_order, a.scalar_scale));
+    store_output(slab_output(a), (size_t)m * N + n0 + r, acc[0]);
 }
 
 // Any K, any alignment: one wave per output column, scalar loads.
@@ -308,7 +383,14 @@ static hipError_t launch_vec(const SlabParams& a, hipStream_t s)
     // among 1..8 x 2..8.
     constexpr int R = 2, KCH = 4;
     const uint32_t blocks = (a.N + 4 * R - 1) / (4 * R);
-    hipLaunchKernelGGL((slab_vec_kernel<MP, R, KCH, TI, TW>), dim3(blocks), dim3(256), 0, s, a);
+    constexpr uint32_t KB = 64 * KCH * Vec16<TW>::n;
+    if constexpr (MP <= 2 || (MP <= 4 && sizeof(TI) == 2)) {
+        if (a.N % (4 * R) == 0 && a.K % KB == 0)
+            hipLaunchKernelGGL((slab_reg_kernel<MP, R, KCH, TI, TW, true>), dim3(blocks), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((slab_reg_kernel<MP, R, KCH, TI, TW, false>), dim3(blocks), dim3(256), 0, s, a);
+    } else
+        hipLaunchKernelGGL((slab_vec_kernel<MP, R, KCH, TI, TW>), dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -330,7 +412,9 @@ bool slab_vec_ok(const SlabParams& a)
 
 hipError_t slab_launch(const SlabParams& a, hipStream_t s)
 {
-    if (a.M >= 2 && gemv_mfma_ok(a)) {
+    // fp16 M 3-4: the vector kernel, dot products on v_dot2 (7.7 us on config
+    // 2 at M = 4 against 8.8 us for the MFMA kernel); M >= 5: the MFMA kernel.
+    if (a.M >= 5 && gemv_mfma_ok(a)) {
         static PerDevice lds_once;   // 64 KB dynamic + the static partial-sum array
         hipError_t e = set_max_lds(lds_once, (const void*)gemv_lds_kernel, 65536);
         if (e != hipSuccess) return e;

@@ -1,4 +1,5 @@
 // nodes.cpp -- prepare()/run() of the matmul-path nodes.
+#include <cstring>
 #include "nodes.h"
 
 #include <cmath>
@@ -134,10 +135,17 @@ void Linear::prepare()
     (*this)["out0"] = Tensor(shape, outputDtype());
 
     vai_linear_args a = args(false);
-    // Prefill shapes (M > 8) stream a fragment-major copy of the weight into
-    // the matrix cores; it is made once per weight buffer and layout (a fused
-    // gate changes the layout), as the reference prepares its weights once.
-    const size_t pbytes = M_ > 8 ? vai_linear_packed_weight_size(&a) : 0;
+    // Prefill shapes and decode GEMVs of 3-8 rows stream a fragment-major copy
+    // of the weight into the matrix cores; it is made once per weight buffer
+    // and layout (a fused gate changes the layout), as the reference prepares
+    // its weights once. The library's plan says whether this shape uses it.
+    vai_linear_args probe = a;
+    probe.packed_weight = reinterpret_cast<void*>(256);
+    char probeName[64] = {0};
+    uint32_t probeSplits = 0;
+    const bool usesPacked = vai_linear_plan(&probe, probeName, sizeof probeName, &probeSplits) == VAI_OK &&
+                            std::strstr(probeName, "packed") != nullptr;
+    const size_t pbytes = usesPacked ? vai_linear_packed_weight_size(&a) : 0;
     if (pbytes && (!packed_ || packedFrom_ != w.uploadId() || packedGated_ != (a.gated != 0))) {
         packed_ = bufferPool().requestBuffer(pbytes);
         vai_linear_args pa = a;

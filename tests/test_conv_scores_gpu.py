@@ -113,6 +113,8 @@ def run_scores(capi, q, k, **kw):
     (2, 2, 130, 130, 16, True, 24, np.float32),      # sliding window
     (1, 1, 70, 90, 48, False, 0, np.float32),        # no mask
     (3, 3, 257, 257, 128, True, 0, np.float16),
+    (12, 4, 130, 130, 64, True, 0, np.float16),      # 12 heads: a partial second round over the 8 XCDs
+    (17, 17, 64, 96, 64, False, 0, np.float16),
 ])
 def test_scores(gpu, hq, hkv, tq, tkv, d, causal, span, dt):
     rng = np.random.default_rng(0)

@@ -213,7 +213,7 @@ def build_cases(capi, stream, which):
         fna.keep = [q, k, v, o, aa, wsa]
         flops = 4 * 8 * 256 * (1024 * 1025 // 2)   # QK^T and P.V over the visible (causal) pairs
         cases["attn"] = Case("attention Q,K,V[8,1024,256] fp16 causal, O = softmax(QK^T/16) V fp16 (fused)", "TFLOP/s",
-                             flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fna, "attention_fwd_kernel<256> + attention_merge_kernel<256> (key range split in 256-key chunks)", flops,
+                             flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fna, "attention_fwd_kernel<256> + attention_merge_kernel<256> (key range split over workgroups, merged by a second pass)", flops,
                              4 * 8 * 1024 * 256 * 2, "f16", "attn")
 
     if "5" in which:   # YOLOX 3x3 conv, bias + SiLU

@@ -1,46 +1,139 @@
 // attention.hip -- fused attention forward O = softmax(scale * Q K^T + mask) V
 // for fp16 Q/K/V on gfx950 (the role of /root/reference/vai/shaders/
 // attention-fa.comp: scores, online softmax and P.V in one pass; the mask
-// rule of common/causal_mask.h:25-42; the node at nodes/attention.h:979-1304).
+// rule of common/causal_mask.h:25-42; the node at nodes/attention.h:979-1304;
+// the key-split merge of attention-fa-reduce.comp).
 //
-// One workgroup (4 waves) owns 64 query rows of one head, 16 per wave, and
-// walks the key tiles (64 keys) the mask leaves visible. Per key tile:
-//  * K [64 x D] and V^T [D x 64] are staged in LDS (V transposed on the way,
-//    so a lane reads its P.V operand as two 8-byte runs);
-//  * S^T = K Q^T on v_mfma_f32_16x16x32_f16 (A = K rows from LDS, B = the
-//    wave's Q rows, held in registers for the whole walk). S^T rather than S:
-//    the output then gives lane l query row l % 16 and 16 of the tile's keys
-//    (16f + 4*(l/16) + r), which is exactly the A operand of the P.V MFMA
-//    with the keys of a 32-wide step in the order 4g + r, 16 + 4g + r; V is
-//    read in the same key order, so each product is still summed once;
-//  * online softmax per query row (running max m and sum l in fp32; row
-//    reductions are two cross-lane exchanges), exp2 with scale * log2(e)
-//    folded in;
-//  * O += P V with P rounded to fp16 (the fp16 operand of the reference's
-//    P.V stage), O in fp32 registers: D/16 fragments of 16x16.
-// The rows a lane holds in O (4*(l/16) + r) differ from its softmax row
-// (l % 16): the per-row rescale and the final 1/l move across lanes by
-// shuffle. Rows with no visible key give 0. The next key tile's global loads
-// are issued into registers before the current tile is computed.
+// One workgroup (4 waves) owns 128 query rows of one head, 32 per wave, and
+// walks the 64-key tiles the mask leaves visible (or one chunk of them when
+// the key range is split over workgroups). Everything runs on
+// v_mfma_f32_32x32x16_f16 in transposed form, so that no value moves between
+// lanes except for one exchange per row reduction:
+//  * S^T = K Q^T: A = 32 keys x 16 head-dim values read from LDS, B = the
+//    wave's 32 query rows, held in registers for the whole walk. Lane l gets
+//    query l % 32 and 16 keys of each 32-key block (4 (l / 32) + {0-3, 8-11,
+//    16-19, 24-27}); with its partner lane l ^ 32 it holds the query's whole
+//    tile row, so the online softmax (running max m and sum l in fp32, exp2
+//    with scale * log2(e) folded in) needs one exchange per reduction.
+//  * O^T += V^T P^T: B = P^T, which is exactly the S^T accumulator layout
+//    rounded to fp16 (the fp16 P operand of the reference's P.V stage),
+//    taken 8 registers at a time; A = 32 head-dim values x 16 keys of V^T,
+//    read from V's row-major LDS tile with ds_read_b64_tr_b16 (4 keys of one
+//    column per lane per read) in the key order the P^T registers hold. O^T
+//    gives lane l query l % 32 again, so the per-row rescale and the final
+//    1/l use the lane's own m and l. O^T lives in accumulation registers,
+//    D/32 fragments of 32x32.
+//  * K and V tiles (row-major, 16-byte chunks XOR-swizzled by row) are copied
+//    global -> LDS by buffer_load ... lds, double buffered: the copies of tile
+//    t + 2 are issued as soon as every wave has finished reading tile t.
+// Rows with no visible key give 0.
 #include <algorithm>
 
 #include "device_common.h"
 #include "kernels.h"
 #include "launch_once.h"
 
+#define LDS_AS __attribute__((address_space(3)))
+
 namespace vai_dev {
 
 namespace fa {
-constexpr int BQ = 64, BKV = 64;
+constexpr int NW = 4, QW = 32, BQ = NW * QW, BKV = 64;
 template <int D> struct Lds {
-    static constexpr int KP = D + 8;              // K row pitch (halves): rows 16 B apart in banks
-    static constexpr int VP = BKV + 8;            // V^T row pitch (halves)
-    static constexpr int K_BYTES = BKV * KP * 2;
-    static constexpr int BYTES = K_BYTES + D * VP * 2;
+    static constexpr int ROWB = D * 2;                  // bytes per K or V row
+    static constexpr int CH = D / 8;                    // 16-byte chunks per row
+    static constexpr int TILE = BKV * ROWB;             // one operand, one tile
+    static constexpr int STAGE = 2 * TILE;              // K then V
+    static constexpr int BYTES = 2 * STAGE;             // double buffered
+    static constexpr int COPIES = TILE / 1024 / NW;     // 1 KB copies per wave and operand
 };
+// Physical 16-byte chunk of logical chunk c in row r: the low three chunk
+// bits XOR f(r % 8), f = 0 2 4 6 1 3 5 7. Eight rows read at one chunk (the
+// K fragments) land on eight distinct chunks of a 128-byte line; four rows
+// read at a pair of chunks (the V^T fragments) on four distinct pairs. The
+// swizzle stays inside 128-byte lines and is its own inverse.
+__host__ __device__ constexpr int swz_f(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
+__host__ __device__ constexpr int swz(int r, int c) { return (c & ~7) | ((c & 7) ^ swz_f(r & 7)); }
 }
 
-typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+// LDS fragment reads of the main loop, as inline asm. The compiler's wait
+// insertion makes its ds_read_b64_tr_b16 builtin wait for every LDS DMA in
+// flight (vmcnt(0)), which would hold each tile's V^T reads until the next
+// tile's copies have landed, and with no registers to spare at D = 256 it
+// sinks prefetched reads down to their MFMAs. The reads below are invisible
+// to that pass: fa_lgkm_wait<N> (N = LDS operations issued since the reads
+// needed) waits for them, and fa_pin ties each fragment to the wait so that
+// its MFMA cannot be scheduled above it. LDS operations complete in order;
+// the loop issues no scalar memory loads (which share the counter out of
+// order). The compiler's own waits only count more operations than it knows
+// of, which makes them stricter.
+template <int OFF>
+__device__ __forceinline__ half8 lds_read128(uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+    half8 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+
+// ds_read_b64_tr_b16 (gfx950): per 16-lane group, result lane j element k is
+// element j % 4 of the 8 bytes that source lane 4 k + j / 4 points at.
+template <int OFF>
+__device__ __forceinline__ half4 lds_read_tr16(uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+    half4 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+
+template <int N>
+__device__ __forceinline__ void fa_lgkm_wait()
+{
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+}
+
+__device__ __forceinline__ void fa_pin(half8& v) { asm volatile("" : "+v"(v)); }
+
+// K fragment of S^T step IDX (key block IDX % 2, head-dim step s = IDX / 2):
+// lane (ql, hf) reads key row 32 (IDX % 2) + ql, head-dim values 16 s + 8 hf
+// .. +7, i.e. logical chunk 2 s + hf. With the row's swizzle f(ql % 8) the
+// lane part is kaddr[s % 4] = stage + ql ROWB + ((2 (s % 4) + hf) ^ f) 16;
+// the rest is the immediate 32 (IDX % 2) ROWB + (s / 4) 128.
+template <int D, int IDX>
+__device__ __forceinline__ half8 fa_kfrag(const uint32_t (&kaddr)[4])
+{
+    constexpr int S = IDX >> 1;
+    return lds_read128<32 * (IDX & 1) * fa::Lds<D>::ROWB + (S >> 2) * 128>(kaddr[S & 3]);
+}
+
+// V^T fragment of key step KK, head-dim block DD: two transposed 8-byte reads
+// of keys 16 KK + 8 part + vkey + vrow, head-dim values 32 DD + vcol .. +3
+// (logical chunk 4 DD + vcol / 8). The lane part is vaddr[DD % 2] = stage +
+// TILE-relative row (vkey + vrow) ROWB + ((4 (DD % 2) + vcol / 8) ^ f) 16 +
+// (vcol % 8) 2; the immediate adds the V tile, (16 KK + 8 part) ROWB and
+// (DD / 2) 128.
+template <int D, int KK, int DD>
+__device__ __forceinline__ half8 fa_vfrag(const uint32_t (&vaddr)[2])
+{
+    using L = fa::Lds<D>;
+    constexpr int base = L::TILE + 16 * KK * L::ROWB + (DD >> 1) * 128;
+    const half4 h0 = lds_read_tr16<base>(vaddr[DD & 1]);
+    const half4 h1 = lds_read_tr16<base + 8 * L::ROWB>(vaddr[DD & 1]);
+    return __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// The dispatcher deals workgroups out to the 8 XCDs round-robin (linear
+// workgroup w runs on XCD w % 8). Logical block of w: XCD x takes the
+// contiguous range [x q + min(x, r), ..) of the n blocks (q = n / 8,
+// r = n % 8), so that consecutive units -- one head's query tiles and key
+// chunks, which read the same K, V and Q -- share one XCD's L2.
+__device__ __forceinline__ uint32_t fa_xcd_block(uint32_t w, uint32_t n)
+{
+    const uint32_t q = n / 8, r = n % 8, x = w % 8;
+    return x * q + (x < r ? x : r) + w / 8;
+}
 
 // The 64-key tiles query tile qt can see: [tb, te).
 __host__ __device__ inline void fa_tile_range(const AttnParams& p, uint32_t qt, int64_t& tb, int64_t& te)
@@ -60,25 +153,57 @@ __host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt)
     return n <= 0 ? 1u : ((uint32_t)n + p.chunk_tiles - 1) / p.chunk_tiles;
 }
 
+// K / V tile copies of key rows [row0, row0 + 64) into stage t % 2: copy j
+// of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB); rows past Tkv
+// read as zero (buffer range check).
 template <int D>
-__global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
+__device__ __forceinline__ void fa_issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, LDS_AS char* lds,
+                                         const uint32_t* coff, int row0, int t, int wave)
+{
+    using L = fa::Lds<D>;
+    LDS_AS char* st = lds + (t & 1) * L::STAGE + wave * L::COPIES * 1024;
+#pragma unroll
+    for (int j = 0; j < L::COPIES; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(st + j * 1024), 16, (int)coff[j],
+                                                 row0 * L::ROWB, 0, 0);
+#pragma unroll
+    for (int j = 0; j < L::COPIES; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(st + L::TILE + j * 1024), 16, (int)coff[j],
+                                                 row0 * L::ROWB, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void fa_wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 {
     using namespace fa;
-    constexpr int KP = Lds<D>::KP, VP = Lds<D>::VP, KS = D / 32, DB = D / 16;
+    using L = Lds<D>;
+    constexpr int KS = D / 16, DF = D / 32;   // 16-wide head-dim steps; 32-wide output fragments
     extern __shared__ half8 fa_lds[];
-    half_t* ks = (half_t*)fa_lds;                              // [BKV][KP]
-    half_t* vt = ks + BKV * KP;                                // [D][VP]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int lr = lane & 15, lg = lane >> 4;
+    LDS_AS char* lds = (LDS_AS char*)(LDS_AS void*)fa_lds;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ql = lane & 31, hf = lane >> 5;   // lane's query (of the wave's 32) and lane half
     const uint32_t Tq = p.tq, Tkv = p.tkv;
-    const uint32_t h = blockIdx.y, b = blockIdx.z, nqt = (Tq + BQ - 1) / BQ;
-    // Work unit -> (query tile, key chunk). Units enumerate the query tiles
-    // from the last (the longest causal walks start first), chunk by chunk.
+    const uint32_t nqt = (Tq + BQ - 1) / BQ;
+    // Workgroup -> (unit, head, batch) with the units of one head on one XCD
+    // (fa_xcd_block), then unit -> (query tile, key chunk). Units enumerate
+    // the query tiles from the last (the longest causal walks start first),
+    // chunk by chunk.
+    const uint32_t X = gridDim.x, HX = X * gridDim.y;
+    const uint32_t lb = fa_xcd_block(blockIdx.x + X * (blockIdx.y + gridDim.y * blockIdx.z), HX * gridDim.z);
+    const uint32_t unit = lb % X, h = (lb / X) % gridDim.y, b = lb / HX;
     uint32_t qt, chunk = 0;
     if (p.units == 0) {
-        qt = nqt - 1 - blockIdx.x;
+        qt = nqt - 1 - unit;
     } else {
-        uint32_t u = blockIdx.x;
+        uint32_t u = unit;
         qt = nqt - 1;
         for (;;) {
             const uint32_t nc = fa_chunks(p, qt);
@@ -87,21 +212,14 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
             --qt;
         }
         chunk = u;
-        qt = __builtin_amdgcn_readfirstlane(qt);
-        chunk = __builtin_amdgcn_readfirstlane(chunk);
     }
+    qt = __builtin_amdgcn_readfirstlane(qt);
+    chunk = __builtin_amdgcn_readfirstlane(chunk);
     const uint32_t q0 = qt * BQ;
     const uint32_t hk = h / (p.hq / p.hkv);
     const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
-    const half_t* K = (const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D;
-    const half_t* V = (const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * D;
 
-    // this wave's 16 query rows as the B operand of S^T = K Q^T
-    const uint32_t qrow = q0 + wave * 16 + lr;
-    half8 qf[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-        qf[s] = qrow < Tq ? *(const half8*)(Q + (size_t)qrow * D + s * 32 + lg * 8) : (half8)0;
+    const uint32_t qrow = q0 + wave * QW + ql;
 
     // visible key tiles of the query tile, then this unit's chunk of them
     int64_t tb, te;
@@ -111,144 +229,248 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p)
         te = std::min<int64_t>(te, c0 + p.chunk_tiles);
         tb = c0;
     }
-    const int64_t kbeg = tb * BKV, kend = std::min<int64_t>(te * BKV, (int64_t)Tkv);
+    const int ntiles = (int)__builtin_amdgcn_readfirstlane((int)std::max<int64_t>(te - tb, 0));
+
+    // K / V tile copies: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
+    // lane l's 16 bytes land at physical chunk pc of row r and come from
+    // logical chunk swz(r, pc) of that row (the swizzle is its own inverse).
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D), (short)0, (int)((size_t)Tkv * D * 2),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * D), (short)0, (int)((size_t)Tkv * D * 2),
+        0x00020000);
+    uint32_t coff[L::COPIES];
+#pragma unroll
+    for (int j = 0; j < L::COPIES; ++j) {
+        const int byte = (wave * L::COPIES + j) * 1024 + lane * 16;
+        const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16;
+        coff[j] = (uint32_t)(r * L::ROWB + swz(r, pc) * 16);
+    }
+    const auto issue = [&](int t) __attribute__((always_inline)) {
+        fa_issue<D>(rk, rv, lds, coff, (int)(tb + t) * BKV, t, wave);
+    };
 
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
-    // this lane's query row reads keys [row_kbeg, row_kend)
     const uint32_t qclip = qrow < Tq ? qrow : Tq - 1;
     const int64_t row_kend = p.mask.key_end(qclip), row_kbeg = p.mask.key_start(qclip);
     float m = -__builtin_inff(), l = 0.f;
-    float4v o[DB];
+    float16v o[DF];
 #pragma unroll
-    for (int d = 0; d < DB; ++d) o[d] = (float4v)0.f;
+    for (int d = 0; d < DF; ++d) o[d] = (float16v)0.f;
 
-    // Key tile j0 is loaded into registers one tile ahead (its global loads
-    // fly while the tile before it is computed), then written to LDS: K
-    // rows as 16-byte chunks, V transposed. K chunk c of a thread is row
-    // c / NC, chunk c % NC (coalesced rows, conflict-free 16-byte writes). V
-    // chunks go 8 keys x 8 chunks per 64 lanes: each load instruction reads
-    // eight 128-byte row pieces, and the transposed 2-byte writes of one
-    // instruction land on consecutive keys of 8 V^T rows (one chunk per row
-    // across the lanes would put 64 lanes on two bank positions).
-    constexpr int NC = D / 8;                  // 16-byte chunks per row
-    constexpr int CPT = BKV * NC / 256;        // chunks per thread and operand
-    half8 kreg[CPT], vreg[CPT];
-    auto vmap = [&](int i, int& r, int& ch) __attribute__((always_inline)) {
-        const int slot = (tid >> 6) + 4 * i, l = tid & 63;   // slot: 64-lane group, 0 .. NC-1
-        r = (slot % 8) * 8 + l / 8;
-        ch = (slot / 8) * 8 + l % 8;
-    };
-    auto load_tile = [&](int64_t j0) __attribute__((always_inline)) {
+    // V^T fragment reads: in each 16-lane group g the transposed read gives
+    // lane j head-dim value dg + j and 4 consecutive keys; source lane s of
+    // the group points at key (base + s / 4), values dg + 4 (s % 4) .. +3.
+    const int g = lane >> 4, s16 = lane & 15;
+    const int vrow = s16 >> 2, vcol = 16 * (g & 1) + 4 * (s16 & 3);   // + 32 d; key + 16 kk + 8 part
+    const int vkey = 4 * (g >> 1);
+    // lane parts of the fragment addresses (fa_kfrag, fa_vfrag), stage 0
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+    uint32_t kofs[4], vofs[2];
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * 256, r = c / NC, ch = c % NC;
-            int vr, vc;
-            vmap(i, vr, vc);
-            kreg[i] = j0 + r < (int64_t)Tkv ? *(const half8*)(K + (size_t)(j0 + r) * D + ch * 8) : (half8)0;
-            vreg[i] = j0 + vr < (int64_t)Tkv ? *(const half8*)(V + (size_t)(j0 + vr) * D + vc * 8) : (half8)0;
-        }
-    };
-    if (kbeg < kend) load_tile(kbeg);
-    for (int64_t j0 = kbeg; j0 < kend; j0 += BKV) {
-        __syncthreads();   // the previous tile's reads are done
+    for (int j = 0; j < 4; ++j) kofs[j] = lds0 + ql * L::ROWB + ((2 * j + hf) ^ swz_f(ql & 7)) * 16;
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * 256, r = c / NC, ch = c % NC;
-            *(half8*)(ks + r * KP + ch * 8) = kreg[i];
-            int vr, vc;
-            vmap(i, vr, vc);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vt[(vc * 8 + e) * VP + vr] = vreg[i][e];
-        }
-        __syncthreads();
-        if (j0 + BKV < kend) load_tile(j0 + BKV);
+    for (int j = 0; j < 2; ++j)
+        vofs[j] = lds0 + (vkey + vrow) * L::ROWB + ((4 * j + (vcol >> 3)) ^ swz_f((vkey + vrow) & 7)) * 16 +
+                  (vcol & 7) * 2;
 
-        // S^T for the 4 key blocks of 16: lane holds query row lr, keys 16f + 4lg + r
-        float4v st[4];
+    // Tile 0's copies, then this wave's 32 query rows as the B operand of
+    // S^T = K Q^T (lane l: query l % 32, head-dim values 16 s + 8 (l / 32)
+    // .. +7 of step s), both waited for in full: the count-based waits below
+    // then see only LDS copies in flight, which complete in order among
+    // themselves (no assumption about their order against loads into VGPRs).
+    if (ntiles > 0) issue(0);
+    half8 qf[KS];
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            st[f] = (float4v)0.f;
+    for (int s = 0; s < KS; ++s)
+        qf[s] = qrow < Tq ? *(const half8*)(Q + (size_t)qrow * D + s * 16 + hf * 8) : (half8)0;
+    fa_wait_vmcnt<0>();
+    if (ntiles > 1) issue(1);
+    for (int t = 0; t < ntiles; ++t) {
+        // tile t landed in every wave's share (tile t + 1's copies may be in flight)
+        if (t > 0) {
+            if (t + 1 < ntiles) fa_wait_vmcnt<2 * L::COPIES>();
+            else fa_wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+        const uint32_t sb = (t & 1) * L::STAGE;
+        uint32_t kaddr[4], vaddr[2];
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const half8 ka = *(const half8*)(ks + (16 * f + lr) * KP + s * 32 + lg * 8);
-                st[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[s], st[f], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) kaddr[j] = kofs[j] + sb;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vaddr[j] = vofs[j] + sb;
+        const int64_t j0 = (tb + t) * BKV;
+
+        // S^T for the tile's two 32-key blocks. Step i of the 2 KS MFMAs is
+        // key block i % 2, head-dim step i / 2 (two independent accumulation
+        // chains); K fragments are read in groups of G, the next group's
+        // reads in flight behind the current group's MFMAs.
+        constexpr int NS = 2 * KS, G = NS < 8 ? NS : (D == 256 ? 4 : 8);
+        float16v sacc[2] = {(float16v)0.f, (float16v)0.f};
+        half8 ka[2][G];
+        static_for<G>([&](auto I) __attribute__((always_inline)) { ka[0][I] = fa_kfrag<D, I>(kaddr); });
+        static_for<NS / G>([&](auto GI) __attribute__((always_inline)) {
+            constexpr int gi = GI, cur = gi & 1;
+            if constexpr (gi + 1 < NS / G) {
+                static_for<G>([&](auto I) __attribute__((always_inline)) {
+                    ka[cur ^ 1][I] = fa_kfrag<D, (gi + 1) * G + I>(kaddr);
+                });
+                fa_lgkm_wait<G>();
+            } else {
+                fa_lgkm_wait<0>();
             }
-        }
-        // mask, scale, running max
+#pragma unroll
+            for (int i = 0; i < G; ++i) fa_pin(ka[cur][i]);
+#pragma unroll
+            for (int i = 0; i < G; ++i) {
+                const int idx = gi * G + i;
+                sacc[idx & 1] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[cur][i], qf[idx >> 1], sacc[idx & 1], 0, 0, 0);
+            }
+        });
+        // first key step's V^T fragments, read while the softmax runs (after
+        // it at D = 256, where the registers would not hold them)
+        constexpr bool VPRE = D < 256;
+        half8 vb[2][DF];
+        if constexpr (VPRE)
+            static_for<DF>([&](auto DD) __attribute__((always_inline)) { vb[0][DD] = fa_vfrag<D, 0, DD>(vaddr); });
+
+        // Online softmax in log2 units (scores x scale x log2 e). Keys of the
+        // tile: kb*32 + 8 (rr / 4) + 4 hf + rr % 4. Tiles wholly visible to
+        // every row of the wave (the mask's interior) with a non-negative
+        // scale take the short path: the max over the raw scores, then
+        // 2^(fma(s, scale', -m)). Others scale and mask first.
+        const bool fast = __all(j0 >= row_kbeg && j0 + BKV <= row_kend) && sl2 >= 0.f;
         float tmax = -__builtin_inff();
+        if (fast) {
 #pragma unroll
-        for (int f = 0; f < 4; ++f)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t kpos = j0 + 16 * f + 4 * lg + r;
-                const bool hide = kpos >= row_kend || kpos < row_kbeg;
-                const float v = hide ? -__builtin_inff() : st[f][r] * sl2;
-                st[f][r] = v;
-                tmax = fmaxf(tmax, v);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+                for (int rr = 0; rr < 16; ++rr) tmax = fmaxf(tmax, sacc[kb][rr]);
+            tmax *= sl2;
+        } else {
+            // visible local keys [lo, hi) of the tile, clamped into [-1, 65]
+            const int lo = (int)std::min<int64_t>(std::max<int64_t>(row_kbeg - j0, -1), 65);
+            const int hi = (int)std::min<int64_t>(std::max<int64_t>(row_kend - j0, -1), 65);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int rr = 0; rr < 16; ++rr) {
+                    const int kl = kb * 32 + 8 * (rr >> 2) + 4 * hf + (rr & 3);
+                    const float v = (kl >= hi || kl < lo) ? -__builtin_inff() : sacc[kb][rr] * sl2;
+                    sacc[kb][rr] = v;
+                    tmax = fmaxf(tmax, v);
+                }
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(m, tmax);
-        const float alpha = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+        // Lazy rescaling: the reference m of a row (the exponent offset of
+        // its O and l) moves only when the row max exceeds it by more than
+        // 8, and then for the whole wave at once (a uniform branch), so that
+        // most tiles skip rescaling O. P = 2^(s - m) then stays below 2^8;
+        // fp16 keeps the same relative precision there, and O / l does not
+        // depend on m. A row with no visible key yet has m = -inf: its first
+        // key moves m; until then 2^(-inf - 0) = 0 keeps P, O and l zero.
+        if (__any(tmax > m + 8.f)) {
+            const float mnew = fmaxf(m, tmax);
+            const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -__builtin_inff() ? 0.f : mnew));
+            l *= alpha;
+            m = mnew;
+#pragma unroll
+            for (int d = 0; d < DF; ++d) o[d] *= alpha;
+        }
+        const float mref = m == -__builtin_inff() ? 0.f : m;
         float psum = 0.f;
-        half8 pa[2];
+        half8 pb[4];   // P^T operand of key step kk: registers 8 (kk % 2) .. +7 of block kk / 2
+        if (fast) {
 #pragma unroll
-        for (int f = 0; f < 4; ++f)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = st[f][r] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(st[f][r] - mnew);
-                psum += e;
-                pa[f / 2][(f % 2) * 4 + r] = (half_t)e;
-            }
-        psum += __shfl_xor(psum, 16, 64);
+                for (int rr = 0; rr < 16; ++rr) {
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][rr], sl2, -mref));
+                    psum += e;
+                    pb[2 * kb + (rr >> 3)][rr & 7] = (half_t)e;
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int rr = 0; rr < 16; ++rr) {
+                    const float e = __builtin_amdgcn_exp2f(sacc[kb][rr] - mref);
+                    psum += e;
+                    pb[2 * kb + (rr >> 3)][rr & 7] = (half_t)e;
+                }
+        }
         psum += __shfl_xor(psum, 32, 64);
-        l = alpha * l + psum;
-        m = mnew;
+        l += psum;
 
-        // O rows 4lg + r take the rescale of their softmax row (held by lane 4lg + r)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float ar = __shfl(alpha, 4 * lg + r, 64);
-#pragma unroll
-            for (int d = 0; d < DB; ++d) o[d][r] *= ar;
-        }
-        // O += P V: k-step s2 covers keys 32 s2 + {4lg + r, 16 + 4lg + r}
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int d = 0; d < DB; ++d) {
-                const half_t* vr = vt + (d * 16 + lr) * VP + 32 * s2 + 4 * lg;
-                const half4v lo = *(const half4v*)vr, hi = *(const half4v*)(vr + 16);
-                const half8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[s2], vb, o[d], 0, 0, 0);
+        // O^T += V^T P^T over the tile's four 16-key steps, the next step's
+        // V^T fragments in flight behind the current step's MFMAs
+        if constexpr (!VPRE)
+            static_for<DF>([&](auto DD) __attribute__((always_inline)) { vb[0][DD] = fa_vfrag<D, 0, DD>(vaddr); });
+        static_for<4>([&](auto KK) __attribute__((always_inline)) {
+            constexpr int kk = KK, cur = kk & 1;
+            if constexpr (kk + 1 < 4) {
+                static_for<DF>([&](auto DD) __attribute__((always_inline)) {
+                    vb[cur ^ 1][DD] = fa_vfrag<D, kk + 1, DD>(vaddr);
+                });
+                fa_lgkm_wait<(2 * DF < 15 ? 2 * DF : 15)>();
+            } else {
+                fa_lgkm_wait<0>();
             }
+#pragma unroll
+            for (int d = 0; d < DF; ++d) fa_pin(vb[cur][d]);
+#pragma unroll
+            for (int d = 0; d < DF; ++d)
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[cur][d], pb[kk], o[d], 0, 0, 0);
+        });
+        // every wave is done reading stage t & 1 before tile t + 2 overwrites it
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (t + 2 < ntiles) issue(t + 2);
     }
 
-    if (p.units != 0) {
-        // partial result: O unnormalised, (m, l) per row
-        const size_t gid = ((size_t)b * p.hq + h) * p.units + blockIdx.x;
-        float* wo = p.ws_o + gid * BQ * D;
+    // Output: a partial (O unnormalised, (m, l) per row) when the key range
+    // is split, else O / l. O^T fragment d gives lane (ql, hf) query ql,
+    // head-dim values 32 d + 8 q4 + 4 hf .. +3 of register group q4. The
+    // wave's 32 rows are contiguous in either destination, so they go out
+    // through LDS: written as fp32 rows (16-byte chunk c of row r at slot
+    // c ^ (r % 16), conflict-free both ways), read back as whole rows, stored
+    // 64 lanes x 16 contiguous bytes at a time. The last tile's barrier
+    // already saw every wave's reads of the K / V stages; each wave then
+    // uses its own 32 QW D bytes (the four regions are exactly the stages).
+    constexpr int CR = D / 4;   // 16-byte fp32 chunks per row
+    LDS_AS float4v* ob = (LDS_AS float4v*)(lds + wave * QW * D * 4);
+    const bool partial = p.units != 0;
+    const float inv = partial ? 1.0f : (l > 0.f ? 1.0f / l : 0.f);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+    for (int d = 0; d < DF; ++d)
 #pragma unroll
-            for (int d = 0; d < DB; ++d) wo[(size_t)(wave * 16 + 4 * lg + r) * D + d * 16 + lr] = o[d][r];
-        if (lg == 0) {
-            float* wml = p.ws_ml + (gid * BQ + wave * 16 + lr) * 2;
-            wml[0] = m;
-            wml[1] = l;
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int c = 8 * d + 2 * q4 + hf;
+            const float4v v = {o[d][4 * q4] * inv, o[d][4 * q4 + 1] * inv, o[d][4 * q4 + 2] * inv,
+                               o[d][4 * q4 + 3] * inv};
+            ob[ql * CR + (c ^ (ql & 15))] = v;
         }
-        return;
+    const size_t gid = ((size_t)b * p.hq + h) * p.units + unit;
+    if (partial && hf == 0) {
+        float* wml = p.ws_ml + (gid * BQ + wave * QW + ql) * 2;
+        wml[0] = m;
+        wml[1] = l;
     }
-    // O / l per row, then the store: lane holds rows 4lg + r, column d*16 + lr
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const uint32_t wrow0 = q0 + wave * QW;   // the wave's first query row
+    const size_t row0 = partial ? gid * BQ + wave * QW : ((size_t)b * p.hq + h) * Tq + wrow0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float ir = __shfl(inv, 4 * lg + r, 64);
-        const uint32_t row = q0 + wave * 16 + 4 * lg + r;
-        if (row >= Tq) continue;
-        const size_t base = (((size_t)b * p.hq + h) * Tq + row) * D + lr;
-#pragma unroll
-        for (int d = 0; d < DB; ++d) st(p.out, p.o_dtype, base + d * 16, o[d][r] * ir);
+    for (int j = 0; j < QW * CR / 64; ++j) {
+        const int e = j * 64 + lane, r = e / CR, c = e % CR;
+        const float4v v = ob[r * CR + (c ^ (r & 15))];
+        const size_t o0 = (row0 + r) * D + 4 * c;
+        if (partial) {
+            *(float4v*)(p.ws_o + o0) = v;
+        } else if (wrow0 + r < Tq) {
+            if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o0) = __builtin_convertvector(v, half4);
+            else *(float4v*)((float*)p.out + o0) = v;
+        }
     }
 }
 
@@ -334,16 +556,45 @@ uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles)
     return units == nqt ? 0u : units;
 }
 
+// Split the key ranges only when the query tiles alone leave CUs idle, in the
+// shortest chunks whose work units still fit one round of workgroups (the
+// merge pass reads every unit's partial O back). At most 64 chunks per query
+// tile (the merge keeps their weights in LDS).
+void attention_plan(AttnParams& p, uint32_t cus)
+{
+    const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ, tiles = p.batch * p.hq * nqt;
+    const uint32_t key_tiles = (p.tkv + fa::BKV - 1) / fa::BKV;
+    const uint32_t min_chunk = std::max<uint32_t>(2, (key_tiles + 63) / 64);
+    p.units = 0;
+    p.chunk_tiles = std::max<uint32_t>(min_chunk, key_tiles);
+    if (tiles >= cus) return;
+    for (uint32_t c = min_chunk; c <= key_tiles; ++c) {
+        const uint32_t u = attention_units(p, c);
+        if (u == 0) return;   // chunks as long as the whole walks: no split
+        if ((uint64_t)u * p.batch * p.hq <= cus) {
+            p.chunk_tiles = c;
+            p.units = u;
+            return;
+        }
+    }
+}
+
 size_t attention_workspace_bytes(const AttnParams& p, uint32_t units)
 {
     return (size_t)p.batch * p.hq * units * fa::BQ * (p.head_dim + 2) * sizeof(float);
+}
+
+void attention_set_workspace(AttnParams& p, void* ws)
+{
+    p.ws_o = (float*)ws;
+    p.ws_ml = p.ws_o + (size_t)p.batch * p.hq * p.units * fa::BQ * p.head_dim;
 }
 
 bool attention_ok(const AttnParams& p)
 {
     return (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256) && p.hq > 0 && p.hkv > 0 &&
            p.hq % p.hkv == 0 && ((uintptr_t)p.q % 16) == 0 && ((uintptr_t)p.k % 16) == 0 &&
-           ((uintptr_t)p.v % 16) == 0;
+           ((uintptr_t)p.v % 16) == 0 && (size_t)p.tkv * p.head_dim * 2 < (1ull << 31);
 }
 
 template <int D>

@@ -409,13 +409,7 @@ static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
         return st;
     p.causal = p.mask.blocks == 1;
     if (!attention_ok(p)) return VAI_ERR_UNSUPPORTED;
-    // Split the key ranges (chunks of 4 tiles = 256 keys) only when the query
-    // tiles alone leave CUs idle.
-    const uint32_t tiles = a->batch * a->hq * ((a->tq + 63) / 64);
-    // at most 64 chunks per query tile (the merge holds their weights in LDS)
-    const uint32_t key_tiles = (a->tkv + 63) / 64;
-    p.chunk_tiles = std::max<uint32_t>(4, (key_tiles + 63) / 64);
-    p.units = tiles < kCUs ? attention_units(p, p.chunk_tiles) : 0;
+    attention_plan(p, kCUs);
     return VAI_OK;
 }
 
@@ -435,8 +429,7 @@ vai_status vai_attention_launch(const vai_attention_args* a, vai_stream_t stream
     if (p.units) {
         const size_t need = attention_workspace_bytes(p, p.units);
         if (!a->workspace || a->workspace_bytes < need) return VAI_ERR_WORKSPACE;
-        p.ws_o = (float*)a->workspace;
-        p.ws_ml = p.ws_o + (size_t)a->batch * a->hq * p.units * 64 * a->head_dim;
+        attention_set_workspace(p, a->workspace);
     }
     return hip_status(attention_launch(p, (hipStream_t)stream));
 }

@@ -166,7 +166,10 @@ bool attention_ok(const AttnParams& p);
 // Units per head for p's shape (0 when no query tile needs splitting), and
 // the workspace the split needs.
 uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles);
+// Chooses the key split (chunk_tiles, units) for a GPU of `cus` compute units.
+void attention_plan(AttnParams& p, uint32_t cus);
 size_t attention_workspace_bytes(const AttnParams& p, uint32_t units);
+void attention_set_workspace(AttnParams& p, void* ws);
 hipError_t attention_launch(const AttnParams& p, hipStream_t s);
 
 // Implicit-GEMM convolution, fp16 weights packed per tap in MFMA fragment order.

@@ -42,6 +42,16 @@ inline __host__ __device__ uint32_t ci32(uint32_t ci) { return (ci + 31) / 32 * 
 inline __host__ __device__ uint32_t cip(uint32_t ci) { return ci32(ci) + 8; }   // LDS row stride (halves)
 }
 
+// LDS of the input band, later reused by the cross-wave sum (the larger of
+// the two); the epilogue's bias and scale follow it.
+__host__ __device__ inline size_t conv_main_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks)
+{
+    const size_t WiP = wi + 2 * (ks / 2), CIP = cv::cip(ci);
+    const size_t stage = (size_t)ks * WiP * CIP * 2;
+    const size_t red = 4ull * cv::CO_TILE * 16 * cv::MAX_WO_FRAGS * 4;
+    return stage > red ? stage : red;
+}
+
 // W [Co, C, k, k] (fp16) -> the fragment-major packed weight: for tap t,
 // 16-channel output block o, 32-channel input block cb and MFMA lane l
 // (output channel o*16 + l%16, input channels cb*32 + 8*(l/16) .. +7):
@@ -81,6 +91,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
     constexpr int PAD = KS / 2;
     const uint32_t WiP = p.wi + 2 * PAD;
     half_t* xs = (half_t*)smem;                              // [KS][WiP][CIP]
+    float* epi_bs = (float*)((char*)smem + conv_main_lds_bytes(p.ci, p.wi, KS));   // [bias x 32, scale x 32]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cw = wave & 3, half = wave >> 2;               // channel-block lane, output-channel half
     const uint32_t co0 = blockIdx.x * CO_TILE, ho = blockIdx.y, b = blockIdx.z;
@@ -97,6 +108,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
             wa[tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * nblk + cb) * 64 + lane) * 8);
     };
     if ((uint32_t)cw < nblk) load_w(cw);
+    constexpr int EPI_COLS = CO_TILE / 8;   // output channels per wave in the epilogue
 
     // ---- input rows: NCHW -> LDS [row][pad + w][c] ----
     // Work item = 8 channels x 8 columns of one input row: eight 16-byte
@@ -117,21 +129,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
             half8 col[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) col[j] = (half8)(half_t)0;
-            if (row_ok) {
+            if (vec && sizeof(TI) == 2) {
+                // eight unconditional loads (row and channel clamped into the
+                // image, their values zeroed afterwards), issued together:
+                // guarded loads would each wait out a full memory latency
+                typedef TI tv8 __attribute__((ext_vector_type(8)));
+                const int hc = hi < 0 ? 0 : (hi >= (int)p.hi ? (int)p.hi - 1 : hi);
+                tv8 t[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t c = min(c0 + e, p.ci - 1);
+                    t[e] = *(const tv8*)((const TI*)p.x + ((size_t)b * p.ci + c) * plane + (size_t)hc * p.wi + w0);
+                }
+                __builtin_amdgcn_sched_barrier(0);   // all eight issued before the first use
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const bool ok = row_ok && c0 + e < p.ci;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) col[j][e] = ok ? (half_t)t[e][j] : (half_t)0;
+                }
+            } else if (row_ok) {
+                // (fp32 input: eight 32-byte rows at once would not fit the
+                // register budget; one channel at a time)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     if (c0 + e >= p.ci) continue;
                     const TI* src = (const TI*)p.x + ((size_t)b * p.ci + c0 + e) * plane + (size_t)hi * p.wi + w0;
-                    typedef TI tv8 __attribute__((ext_vector_type(8)));
-                    tv8 t;
-                    if (vec) {
-                        t = *(const tv8*)src;
-                    } else {
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) t[j] = w0 + j < p.wi ? src[j] : (TI)0;
-                    }
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) col[j][e] = (half_t)t[j];
+                    for (int j = 0; j < 8; ++j) col[j][e] = w0 + j < p.wi ? (half_t)src[j] : (half_t)0;
                 }
             }
             half_t* dst = xs + ((size_t)r * WiP + PAD + w0) * CIP + c0;
@@ -144,6 +169,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
             const uint32_t cg = i % (C32 / 8), rc = i / (C32 / 8), r = rc / (2 * PAD), e = rc % (2 * PAD);
             const uint32_t w = e < PAD ? e : PAD + p.wi + (e - PAD);
             *(half8*)(xs + ((size_t)r * WiP + w) * CIP + cg * 8) = (half8)(half_t)0;
+        }
+        // bias and scale of the tile's output channels, for the epilogue
+        // (unconditional loads: a missing one reads the packed weight, at
+        // least Co values long, and the epilogue ignores it)
+        if (tid < 2 * CO_TILE) {
+            const half_t* src = tid < CO_TILE ? (p.bias ? (const half_t*)p.bias : p.wp)
+                                              : (p.scale ? (const half_t*)p.scale : p.wp);
+            epi_bs[tid] = (float)src[min(co0 + (tid % CO_TILE), p.co - 1)];
         }
     }
     __syncthreads();
@@ -161,7 +194,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
         if (cb != (uint32_t)cw) load_w(cb);
         const uint32_t cofs = cb * 32 + fg * 8;
 #pragma unroll
-        for (int kh = 0; kh < KS; ++kh) {
+        for (int kh = 0; kh < KS; ++kh)
 #pragma unroll
             for (int kw = 0; kw < KS; ++kw) {
                 const half_t* xrow = xs + ((size_t)kh * WiP + kw) * CIP + cofs;
@@ -173,7 +206,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
                     }
                 }
             }
-        }
     }
     __syncthreads();
 
@@ -189,32 +221,88 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
                 red[((size_t)cw * CO_TILE + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
     __syncthreads();
     const size_t HoWo = (size_t)p.ho * p.wo;
-    for (uint32_t col = tid >> 6; col < (uint32_t)CO_TILE; col += 8) {
-        const uint32_t co = co0 + col;
+    const bool vec4 = p.wo % 4 == 0 && (uintptr_t)p.out % 16 == 0 && (uintptr_t)p.residual % 16 == 0;
+    if (vec4) {
+        // 4 consecutive positions of one output channel per work item: four
+        // 16-byte partial-sum reads, one 16-byte (fp32) or 8-byte (fp16)
+        // store. A row of Wo outputs stays 16-byte aligned (Ho Wo and Wo
+        // are multiples of 4).
+        const uint32_t q4 = p.wo / 4, items = CO_TILE * q4;
+        for (uint32_t it = tid; it < items; it += 512) {
+            const uint32_t col = it / q4, wo = (it % q4) * 4, co = co0 + col;
+            if (co >= p.co) continue;
+            float4v v = *(const float4v*)(red + (size_t)col * rw + wo);
+#pragma unroll
+            for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CO_TILE + col) * rw + wo);
+            const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
+            const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
+            float4v rr = (float4v)0.f;
+            if (p.residual) {
+                if (p.residual_dtype == DT_F16) rr = __builtin_convertvector(*(const half4*)((const half_t*)p.residual + o), float4v);
+                else rr = *(const float4v*)((const float*)p.residual + o);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x = p.scale ? fmaf(v[e], sc, bias) : v[e] + bias;
+                if (p.residual && p.residual_order == 1) x += rr[e];
+                x = epilogue(x, p.epilogue);
+                if (p.residual && p.residual_order == 0) x += rr[e];
+                v[e] = x;
+            }
+            if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(v, half4);
+            else *(float4v*)((float*)p.out + o) = v;
+        }
+        return;
+    }
+    // Outputs (co0 + wave + 8 i, wo = lane + 64 k); residuals first, all
+    // loads in flight together (indices clamped, unused values discarded).
+    constexpr int EPI_W = MAX_WO_FRAGS * 16 / 64;
+    float rv[EPI_COLS][EPI_W] = {};
+    if (p.residual) {
+        const bool r16 = p.residual_dtype == DT_F16;
+#pragma unroll
+        for (int i = 0; i < EPI_COLS; ++i)
+#pragma unroll
+            for (int k = 0; k < EPI_W; ++k) {
+                const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
+                const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
+                rv[i][k] = r16 ? (float)((const half_t*)p.residual)[o] : 0.f;
+            }
+        if (!r16) {
+#pragma unroll
+            for (int i = 0; i < EPI_COLS; ++i)
+#pragma unroll
+                for (int k = 0; k < EPI_W; ++k) {
+                    const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
+                    rv[i][k] = ((const float*)p.residual)[((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo];
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPI_COLS; ++i) {
+        const uint32_t col = wave + 8 * i, co = co0 + col;
         if (co >= p.co) break;
-        const float bias = p.bias ? ld(p.bias, DT_F16, co) : 0.f;
-        const float sc = p.scale ? ld(p.scale, DT_F16, co) : 1.f;
+        const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
         const size_t obase = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo;
-        for (uint32_t wo = lane; wo < p.wo; wo += 64) {
+#pragma unroll
+        for (int k = 0; k < EPI_W; ++k) {
+            const uint32_t wo = lane + 64 * k;
+            if (wo >= p.wo) break;
             float v = red[(size_t)col * rw + wo] + red[((size_t)CO_TILE + col) * rw + wo] +
                       red[((size_t)2 * CO_TILE + col) * rw + wo] + red[((size_t)3 * CO_TILE + col) * rw + wo];
             v = p.scale ? fmaf(v, sc, bias) : v + bias;
-            const size_t o = obase + wo;
-            const float rr = p.residual ? ld(p.residual, p.residual_dtype, o) : 0.f;
+            const float rr = rv[i][k];
             if (p.residual && p.residual_order == 1) v += rr;
             v = epilogue(v, p.epilogue);
             if (p.residual && p.residual_order == 0) v += rr;
-            st(p.out, p.o_dtype, o, v);
+            st(p.out, p.o_dtype, obase + wo, v);
         }
     }
 }
 
 size_t conv_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks)
 {
-    const size_t WiP = wi + 2 * (ks / 2), CIP = cv::cip(ci);
-    const size_t stage = (size_t)ks * WiP * CIP * 2;
-    const size_t red = 4ull * cv::CO_TILE * 16 * cv::MAX_WO_FRAGS * 4;
-    return stage > red ? stage : red;
+    return conv_main_lds_bytes(ci, wi, ks) + 2 * cv::CO_TILE * sizeof(float);
 }
 
 bool conv_nhwc_ok(uint32_t ci, uint32_t wi, uint32_t wo, uint32_t ks)

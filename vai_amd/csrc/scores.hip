@@ -98,7 +98,9 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParam
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
         const int s = (wave * LOADS + i) * 64 + lane;
-        isk[i] = s >= T * CH;
+        // (copies never straddle Q and K, T * CH being a multiple of 64: a
+        // wave-uniform test keeps the descriptor choice scalar)
+        isk[i] = (wave * LOADS + i) * 64 >= T * CH;
         const int ss = isk[i] ? s - T * CH : s;
         const int row = ss / CH, ch = (ss % CH) ^ ((row / RPW) % CH);
         const uint32_t g = min((isk[i] ? n0 : m0) + row, (isk[i] ? N : M) - 1);

@@ -299,9 +299,12 @@ __global__ __launch_bounds__(256, 1) void gemm_big_kernel(GemmParams p)
             });
         }
         {
+            // (tile indices made wave-uniform: the store resource built from
+            // them then lives in SGPRs, not in a waterfall loop per store)
             uint32_t tm, tn;
             order.of(blockIdx.x + (uint32_t)r * G, tm, tn);
-            tile_store<GATED>(p, acc, cb, tm, tn, wm, wn, fr, fk);
+            tile_store<GATED>(p, acc, cb, __builtin_amdgcn_readfirstlane(tm), __builtin_amdgcn_readfirstlane(tn), wm,
+                              wn, fr, fk);
         }
     }
     wait_vmcnt<0>();   // the clamped copies land before the workgroup retires

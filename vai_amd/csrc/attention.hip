@@ -87,6 +87,19 @@ __device__ __forceinline__ half4 lds_read_tr16(uint32_t addr)
     return r;
 }
 
+// x * a for an accumulator element held in an accumulation register, in
+// place: the compiler, given a plain multiply, keeps a VGPR copy of every
+// accumulator live across the whole tile loop for the (rare) rescale and
+// pays 128 register moves per tile at D = 256.
+__device__ __forceinline__ float fa_scale_acc(float x, float a)
+{
+    float t;
+    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                 : "+a"(x), "=&v"(t)
+                 : "v"(a));
+    return x;
+}
+
 template <int N>
 __device__ __forceinline__ void fa_lgkm_wait()
 {
@@ -371,13 +384,15 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         // fp16 keeps the same relative precision there, and O / l does not
         // depend on m. A row with no visible key yet has m = -inf: its first
         // key moves m; until then 2^(-inf - 0) = 0 keeps P, O and l zero.
-        if (__any(tmax > m + 8.f)) {
+        if (__builtin_expect(__any(tmax > m + 8.f), 0)) {
             const float mnew = fmaxf(m, tmax);
             const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -__builtin_inff() ? 0.f : mnew));
             l *= alpha;
             m = mnew;
 #pragma unroll
-            for (int d = 0; d < DF; ++d) o[d] *= alpha;
+            for (int d = 0; d < DF; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[d][r] = fa_scale_acc(o[d][r], alpha);
         }
         const float mref = m == -__builtin_inff() ? 0.f : m;
         float psum = 0.f;

@@ -120,7 +120,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
     {
         const uint32_t ngc = C32 / 8, ngw = (p.wi + 7) / 8, items = KS * ngc * ngw;
         const size_t plane = (size_t)p.hi * p.wi;
-        const bool vec = p.wi % 8 == 0 && ((uintptr_t)p.x % (8 * sizeof(TI))) == 0;
+        const bool vec = p.wi % 8 == 0 && ((uintptr_t)p.x % (8 * sizeof(TI))) == 0 &&
+                         (size_t)p.ci * plane * sizeof(TI) < (1ull << 31);
+        const uint32_t plane_bytes = (uint32_t)(plane * sizeof(TI));
+        const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((const TI*)p.x + (size_t)b * p.ci * plane), (short)0,
+            (int)std::min<size_t>((size_t)p.ci * plane * sizeof(TI), 0x7FFFFFFF), 0x00020000);
         for (uint32_t it = tid; it < items; it += 512) {
             const uint32_t cg = it % ngc, rest = it / ngc, wg = rest % ngw, r = rest / ngw;
             const int hi = (int)(ho * p.stride) + (int)r - PAD;
@@ -130,23 +135,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
 #pragma unroll
             for (int j = 0; j < 8; ++j) col[j] = (half8)(half_t)0;
             if (vec && sizeof(TI) == 2) {
-                // eight unconditional loads (row and channel clamped into the
-                // image, their values zeroed afterwards), issued together:
-                // guarded loads would each wait out a full memory latency
-                typedef TI tv8 __attribute__((ext_vector_type(8)));
-                const int hc = hi < 0 ? 0 : (hi >= (int)p.hi ? (int)p.hi - 1 : hi);
-                tv8 t[8];
+                // eight 16-byte loads issued together through a resource over
+                // the image: channels past Ci fall outside it, and so does a
+                // row outside the image, whose offset is 2^31 plus the channel's
+                // (the image is under 2^31 bytes), so the hardware bounds check
+                // returns their zeros. (Guarded loads would each wait out a
+                // full memory latency.)
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const uint32_t rowoff = row_ok ? (uint32_t)(hi * (int)p.wi + (int)w0) * 2u : 0x80000000u;
+                u32x4 t[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t c = min(c0 + e, p.ci - 1);
-                    t[e] = *(const tv8*)((const TI*)p.x + ((size_t)b * p.ci + c) * plane + (size_t)hc * p.wi + w0);
-                }
+                for (int e = 0; e < 8; ++e)
+                    t[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         xrsrc, (int)(rowoff + (c0 + e) * plane_bytes), 0, 0));
                 __builtin_amdgcn_sched_barrier(0);   // all eight issued before the first use
+                // transpose: column j's channel pair (2k, 2k + 1) is one dword,
+                // the j-th halves of channel 2k's and 2k + 1's column runs
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const bool ok = row_ok && c0 + e < p.ci;
+                for (int j = 0; j < 8; ++j) {
+                    u32x4 v;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) col[j][e] = ok ? (half_t)t[e][j] : (half_t)0;
+                    for (int k = 0; k < 4; ++k)
+                        v[k] = __builtin_amdgcn_perm(t[2 * k + 1][j / 2], t[2 * k][j / 2],
+                                                     (j & 1) ? 0x07060302u : 0x05040100u);
+                    col[j] = __builtin_bit_cast(half8, v);
                 }
             } else if (row_ok) {
                 // (fp32 input: eight 32-byte rows at once would not fit the

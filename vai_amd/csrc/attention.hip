@@ -228,6 +228,12 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     }
     qt = __builtin_amdgcn_readfirstlane(qt);
     chunk = __builtin_amdgcn_readfirstlane(chunk);
+    if (p.units != 0 && chunk == 0 && threadIdx.x == 0) {
+        // the merge pass's index: this query tile's first unit and chunk count
+        uint32_t* tab = p.ws_tab + (((size_t)b * p.hq + h) * nqt + qt) * 2;
+        tab[0] = unit;
+        tab[1] = fa_chunks(p, qt);
+    }
     const uint32_t q0 = qt * BQ;
     const uint32_t hk = h / (p.hq / p.hkv);
     const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
@@ -445,8 +451,11 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         if (t + 2 < ntiles) issue(t + 2);
     }
 
-    // Output: a partial (O unnormalised, (m, l) per row) when the key range
-    // is split, else O / l. O^T fragment d gives lane (ql, hf) query ql,
+    // Output: a partial when the key range is split, else O / l. A partial
+    // is (m, l) per row and O: unnormalised in fp32 for fp32 output (as
+    // attention-fa-reduce.comp keeps it), O / l in fp16 for fp16 output (a
+    // convex combination of V rows, rounded once more before the final fp16
+    // rounding; half the bytes through HBM, which bound the split). O^T fragment d gives lane (ql, hf) query ql,
     // head-dim values 32 d + 8 q4 + 4 hf .. +3 of register group q4. The
     // wave's 32 rows are contiguous in either destination, so they go out
     // through LDS: written as fp32 rows (16-byte chunk c of row r at slot
@@ -456,8 +465,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // uses its own 32 QW D bytes (the four regions are exactly the stages).
     constexpr int CR = D / 4;   // 16-byte fp32 chunks per row
     LDS_AS float4v* ob = (LDS_AS float4v*)(lds + wave * QW * D * 4);
-    const bool partial = p.units != 0;
-    const float inv = partial ? 1.0f : (l > 0.f ? 1.0f / l : 0.f);
+    const bool partial = p.units != 0, part16 = partial && p.o_dtype == DT_F16;
+    const float inv = (partial && !part16) ? 1.0f : (l > 0.f ? 1.0f / l : 0.f);
 #pragma unroll
     for (int d = 0; d < DF; ++d)
 #pragma unroll
@@ -480,7 +489,9 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         const int e = j * 64 + lane, r = e / CR, c = e % CR;
         const float4v v = ob[r * CR + (c ^ (r & 15))];
         const size_t o0 = (row0 + r) * D + 4 * c;
-        if (partial) {
+        if (part16) {
+            *(half4*)((half_t*)p.ws_o + o0) = __builtin_convertvector(v, half4);
+        } else if (partial) {
             *(float4v*)(p.ws_o + o0) = v;
         } else if (wrow0 + r < Tq) {
             if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o0) = __builtin_convertvector(v, half4);
@@ -491,6 +502,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 
 // Merge of the key chunks of one query tile: O = sum_c 2^(m_c - M) O_c /
 // sum_c 2^(m_c - M) l_c, M = max_c m_c (m in log2 units); 0 without keys.
+// With fp16 partials O_c holds O_c / l_c, weighed by 2^(m_c - M) l_c.
 template <int D>
 __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
 {
@@ -500,36 +512,23 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
     __shared__ float wgt[RG][MAXC];
     const uint32_t nqt = (p.tq + BQ - 1) / BQ, qt = blockIdx.x / (BQ / RG), r0 = (blockIdx.x % (BQ / RG)) * RG;
     const uint32_t h = blockIdx.y, b = blockIdx.z;
-    // first unit of query tile qt: the chunks of the later tiles (units run
-    // from the last query tile down), summed across a 64-lane group
-    __shared__ uint32_t first_unit;
-    if (threadIdx.x < 64) {
-        uint32_t n = 0;
-        for (uint32_t q = qt + 1 + threadIdx.x; q < nqt; q += 64) n += fa_chunks(p, q);
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) n += __shfl_xor(n, s, 64);
-        if (threadIdx.x == 0) first_unit = n;
-    }
-    __syncthreads();
-    const uint32_t u0 = first_unit;
-    const uint32_t nc = fa_chunks(p, qt);
+    const uint2 tab = *(const uint2*)(p.ws_tab + (((size_t)b * p.hq + h) * nqt + qt) * 2);
+    const uint32_t u0 = __builtin_amdgcn_readfirstlane(tab.x), nc = __builtin_amdgcn_readfirstlane(tab.y);
     const size_t g0 = ((size_t)b * p.hq + h) * p.units + u0;
-    // per-row chunk weights 2^(m_c - M) / sum_c 2^(m_c - M) l_c: thread t
+    const bool part16 = p.o_dtype == DT_F16;
+    // per-row chunk weights 2^(m_c - M) (l_c) / sum_c 2^(m_c - M) l_c: thread t
     // takes row t / 32 and chunks t % 32, t % 32 + 32; max and sum reduce
     // over the row's 32 lanes
     {
         const uint32_t rl = threadIdx.x / 32, c0 = threadIdx.x % 32, row = r0 + rl;
         float mc[2], lc[2];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t c = c0 + 32 * k;
-            mc[k] = -__builtin_inff();
-            lc[k] = 0.f;
-            if (c < nc) {
-                const float2 ml = *(const float2*)(p.ws_ml + ((g0 + c) * BQ + row) * 2);
-                mc[k] = ml.x;
-                lc[k] = ml.y;
-            }
+        for (int k = 0; k < 2; ++k) {   // both loads in flight (chunks past nc read nc - 1, then dropped)
+            const uint32_t c = min(c0 + 32 * k, nc - 1);
+            const float2 ml = *(const float2*)(p.ws_ml + ((g0 + c) * BQ + row) * 2);
+            const bool in = c0 + 32 * k < nc;
+            mc[k] = in ? ml.x : -__builtin_inff();
+            lc[k] = in ? ml.y : 0.f;
         }
         float M = fmaxf(mc[0], mc[1]);
 #pragma unroll
@@ -539,25 +538,47 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
         for (int k = 0; k < 2; ++k) {
             w[k] = (M == -__builtin_inff() || mc[k] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(mc[k] - M);
             den += w[k] * lc[k];
+            if (part16) w[k] *= lc[k];
         }
 #pragma unroll
         for (int s = 16; s >= 1; s >>= 1) den += __shfl_xor(den, s, 32);
         const float inv = den > 0.f ? 1.0f / den : 0.f;
 #pragma unroll
-        for (int k = 0; k < 2; ++k)
-            if (c0 + 32 * k < nc) wgt[rl][c0 + 32 * k] = w[k] * inv;
+        for (int k = 0; k < 2; ++k) wgt[rl][c0 + 32 * k] = w[k] * inv;   // 0 past nc
     }
     __syncthreads();
-    // thread t: rows r0 + (t*4 / D) .., 4 consecutive columns (16-byte loads)
+    // thread t: rows r0 + (t*4 / D) .., 4 consecutive columns. Chunks 8 at a
+    // time with all eight loads in flight (chunks past nc read chunk nc - 1
+    // and weigh 0; one loop per partial type, so no branch sits between the
+    // loads and their waits).
+    const uint32_t ncr = (nc + 7) & ~7u;
     for (uint32_t e = threadIdx.x * 4; e < RG * D; e += 256 * 4) {
         const uint32_t rl = e / D, col = e % D, qrow = qt * BQ + r0 + rl;
         if (qrow >= p.tq) continue;
+        const size_t base = (g0 * BQ + r0 + rl) * D + col, cstride = (size_t)BQ * D;
         float4v acc = (float4v)0.f;
-        for (uint32_t c = 0; c < nc; ++c)
-            acc += wgt[rl][c] * *(const float4v*)(p.ws_o + ((g0 + c) * BQ + r0 + rl) * D + col);
-        const size_t o = (((size_t)b * p.hq + h) * p.tq + qrow) * D + col;
+        if (part16) {
+            const half_t* src = (const half_t*)p.ws_o + base;
+            for (uint32_t c0 = 0; c0 < ncr; c0 += 8) {
+                half4 v[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) st(p.out, p.o_dtype, o + k, acc[k]);
+                for (int i = 0; i < 8; ++i) v[i] = *(const half4*)(src + min(c0 + i, nc - 1) * cstride);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc += wgt[rl][c0 + i] * __builtin_convertvector(v[i], float4v);
+            }
+        } else {
+            const float* src = p.ws_o + base;
+            for (uint32_t c0 = 0; c0 < ncr; c0 += 8) {
+                float4v v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = *(const float4v*)(src + min(c0 + i, nc - 1) * cstride);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc += wgt[rl][c0 + i] * v[i];
+            }
+        }
+        const size_t o = (((size_t)b * p.hq + h) * p.tq + qrow) * D + col;
+        if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(acc, half4);
+        else *(float4v*)((float*)p.out + o) = acc;
     }
 }
 
@@ -596,13 +617,16 @@ void attention_plan(AttnParams& p, uint32_t cus)
 
 size_t attention_workspace_bytes(const AttnParams& p, uint32_t units)
 {
-    return (size_t)p.batch * p.hq * units * fa::BQ * (p.head_dim + 2) * sizeof(float);
+    const size_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
+    return (size_t)p.batch * p.hq * units * fa::BQ * (p.head_dim + 2) * sizeof(float) +
+           (size_t)p.batch * p.hq * nqt * 2 * sizeof(uint32_t);
 }
 
 void attention_set_workspace(AttnParams& p, void* ws)
 {
     p.ws_o = (float*)ws;
     p.ws_ml = p.ws_o + (size_t)p.batch * p.hq * p.units * fa::BQ * p.head_dim;
+    p.ws_tab = (uint32_t*)(p.ws_ml + (size_t)p.batch * p.hq * p.units * fa::BQ * 2);
 }
 
 bool attention_ok(const AttnParams& p)

@@ -157,10 +157,12 @@ struct AttnParams {
     // Key-range split (0 units: each workgroup walks all of its keys and
     // writes O). Otherwise each query tile's keys are cut into chunks of
     // chunk_tiles 64-key tiles, `units` work units per head; partial O and
-    // (max, sum) go to ws_o / ws_ml and a merge pass combines them.
+    // (max, sum) go to ws_o / ws_ml and a merge pass combines them, finding
+    // each query tile's first unit and chunk count in ws_tab.
     uint32_t units, chunk_tiles;
-    float* ws_o;                  // [batch*hq*units][64][head_dim]
-    float* ws_ml;                 // [batch*hq*units][64][2]
+    float* ws_o;                  // [batch*hq*units][128][head_dim] (fp32, or fp16 O / l for fp16 output)
+    float* ws_ml;                 // [batch*hq*units][128][2]
+    uint32_t* ws_tab;             // [batch*hq*query tiles][2]: first unit, chunks
 };
 bool attention_ok(const AttnParams& p);
 // Units per head for p's shape (0 when no query tile needs splitting), and

@@ -60,7 +60,8 @@ constexpr size_t f32k_lds_bytes()
 // fp32 output, no residual, bias absent or one [N] row: the activation is
 // compile-time (EPI 6: the runtime epilogue code).
 template <int NF, uint32_t EPI>
-__device__ __forceinline__ void f32k_store(const GemmParams& p, const float (&v)[2][NF], uint32_t row, uint32_t col)
+__device__ __forceinline__ void f32k_store(const GemmParams& p, const float (&v)[2][NF], const float (&cbias)[NF],
+                                           uint32_t row, uint32_t col)
 {
     const uint32_t M = p.M, N = p.N;
     const float s = p.scalar_scale;
@@ -68,7 +69,7 @@ __device__ __forceinline__ void f32k_store(const GemmParams& p, const float (&v)
     for (int j = 0; j < NF; ++j) {
         const uint32_t c = col + j * 16;
         if (c >= N) continue;
-        const float cb = p.bias ? ld(p.bias, p.bias_dtype, c) : 0.f;
+        const float cb = cbias[j];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t r = row + i * 16;
@@ -115,6 +116,22 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
     const int c_lo = wave * chunks / WAVES, c_hi = (wave + 1) * chunks / WAVES;
     const int n = c_hi - c_lo;
     LDS_AS char* ring = lds + (size_t)wave * SLOTS * STAGE;
+
+    // The fast epilogue's bias (one [N] row) for this thread's NF columns
+    // c0 + lane % 16 + 16 j, loaded now, unconditionally (columns clamped),
+    // so that its latency hides behind the K loop instead of following it.
+    float cbias[NF];
+#pragma unroll
+    for (int j = 0; j < NF; ++j) cbias[j] = 0.f;
+    if (p.bias) {
+        if (p.bias_dtype == DT_F16) {
+#pragma unroll
+            for (int j = 0; j < NF; ++j) cbias[j] = (float)((const half_t*)p.bias)[min(c0 + (lane & 15) + 16 * j, N - 1)];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NF; ++j) cbias[j] = ((const float*)p.bias)[min(c0 + (lane & 15) + 16 * j, N - 1)];
+        }
+    }
 
     float4v acc[2][NF];
 #pragma unroll
@@ -204,10 +221,10 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
     const bool plain = p.c_dtype == 0 && !p.residual && (!p.bias || p.bias_repeat == N);
     if (plain) {
         switch (p.epilogue) {
-        case 0: f32k_store<NF, 0>(p, v, r0 + row_l, c0 + col_l); break;
-        case 3: f32k_store<NF, 3>(p, v, r0 + row_l, c0 + col_l); break;
-        case 4: f32k_store<NF, 4>(p, v, r0 + row_l, c0 + col_l); break;
-        default: f32k_store<NF, 6>(p, v, r0 + row_l, c0 + col_l); break;
+        case 0: f32k_store<NF, 0>(p, v, cbias, r0 + row_l, c0 + col_l); break;
+        case 3: f32k_store<NF, 3>(p, v, cbias, r0 + row_l, c0 + col_l); break;
+        case 4: f32k_store<NF, 4>(p, v, cbias, r0 + row_l, c0 + col_l); break;
+        default: f32k_store<NF, 6>(p, v, cbias, r0 + row_l, c0 + col_l); break;
         }
         return;
     }

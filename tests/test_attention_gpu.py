@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("b, hq, hkv, tq, tkv, d, causal, span, odt", [
     (1, 8, 8, 1024, 1024, 256, True, 0, np.float32),     # config 4's shape, full attention output
+    (1, 8, 8, 1024, 1024, 256, True, 0, np.float16),     # the bench's attn line: split, fp16 partials
     (1, 8, 2, 200, 200, 128, True, 0, np.float16),       # GQA, row and key tails
     (1, 4, 4, 3, 300, 64, True, 0, np.float32),          # decode-like: 3 new queries over 300 keys
     (1, 2, 1, 257, 257, 64, True, 50, np.float32),       # sliding window
@@ -72,9 +73,9 @@ def test_attention_rejects(gpu):
 
 
 def test_attention_workspace(gpu):
-    """The key-range split asks for a workspace (config 4's shape: 128 query
-    tiles leave CUs idle) and refuses to run without one; a shape whose query
-    tiles fill the GPU needs none."""
+    """The key-range split asks for a workspace (config 4's shape: its 64
+    query tiles of 128 rows leave CUs idle) and refuses to run without one;
+    a shape whose query tiles fill the GPU (32 heads x 8 tiles) needs none."""
     import ctypes
     D = gpu.DeviceArray
     q = D((8, 1024, 256), np.float16)

@@ -100,6 +100,24 @@ __device__ __forceinline__ float fa_scale_acc(float x, float a)
     return x;
 }
 
+// Pairwise tree reductions of 32 values (depth 5 instead of a chain of 31).
+__device__ __forceinline__ float fa_tree_max(float (&v)[32])
+{
+#pragma unroll
+    for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) v[i] = fmaxf(v[i], v[i + w]);
+    return v[0];
+}
+__device__ __forceinline__ float fa_tree_sum(float (&v)[32])
+{
+#pragma unroll
+    for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) v[i] += v[i + w];
+    return v[0];
+}
+
 template <int N>
 __device__ __forceinline__ void fa_lgkm_wait()
 {
@@ -389,13 +407,14 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         // scale take the short path: the max over the raw scores, then
         // 2^(fma(s, scale', -m)). Others scale and mask first.
         const bool fast = __all(j0 >= row_kbeg && j0 + BKV <= row_kend) && sl2 >= 0.f;
-        float tmax = -__builtin_inff();
+        // (reductions as trees: with one wave per SIMD a chain of dependent
+        // steps costs its whole latency)
+        float tv[32];
+        float tmax;
         if (fast) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int rr = 0; rr < 16; ++rr) tmax = fmaxf(tmax, sacc[kb][rr]);
-            tmax *= sl2;
+            for (int i = 0; i < 32; ++i) tv[i] = sacc[i >> 4][i & 15];
+            tmax = fa_tree_max(tv) * sl2;
         } else {
             // visible local keys [lo, hi) of the tile, clamped into [-1, 65]
             const int lo = (int)std::min<int64_t>(std::max<int64_t>(row_kbeg - j0, -1), 65);
@@ -407,8 +426,9 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
                     const int kl = kb * 32 + 8 * (rr >> 2) + 4 * hf + (rr & 3);
                     const float v = (kl >= hi || kl < lo) ? -__builtin_inff() : sacc[kb][rr] * sl2;
                     sacc[kb][rr] = v;
-                    tmax = fmaxf(tmax, v);
+                    tv[kb * 16 + rr] = v;
                 }
+            tmax = fa_tree_max(tv);
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         // Lazy rescaling: the reference m of a row (the exponent offset of
@@ -429,7 +449,6 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
                 for (int r = 0; r < 16; ++r) o[d][r] = fa_scale_acc(o[d][r], alpha);
         }
         const float mref = m == -__builtin_inff() ? 0.f : m;
-        float psum = 0.f;
         half8 pb[4];   // P^T operand of key step kk: registers 8 (kk % 2) .. +7 of block kk / 2
         if (fast) {
 #pragma unroll
@@ -437,7 +456,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 #pragma unroll
                 for (int rr = 0; rr < 16; ++rr) {
                     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][rr], sl2, -mref));
-                    psum += e;
+                    tv[kb * 16 + rr] = e;
                     pb[2 * kb + (rr >> 3)][rr & 7] = (half_t)e;
                 }
         } else {
@@ -446,12 +465,14 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 #pragma unroll
                 for (int rr = 0; rr < 16; ++rr) {
                     const float e = __builtin_amdgcn_exp2f(sacc[kb][rr] - mref);
-                    psum += e;
+                    tv[kb * 16 + rr] = e;
                     pb[2 * kb + (rr >> 3)][rr & 7] = (half_t)e;
                 }
         }
-        psum += __shfl_xor(psum, 32, 64);
-        l += psum;
+        {
+            const float ps = fa_tree_sum(tv);
+            l += ps + __shfl_xor(ps, 32, 64);
+        }
 
         // O^T += V^T P^T over the tile's four 16-key steps, the next step's
         // V^T fragments in flight behind the current step's MFMAs

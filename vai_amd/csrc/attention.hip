@@ -47,13 +47,21 @@ template <int D> struct Lds {
     static constexpr int BYTES = 2 * STAGE;             // double buffered
     static constexpr int COPIES = TILE / 1024 / NW;     // 1 KB copies per wave and operand
 };
-// Physical 16-byte chunk of logical chunk c in row r: the low three chunk
-// bits XOR f(r % 8), f = 0 2 4 6 1 3 5 7. Eight rows read at one chunk (the
-// K fragments) land on eight distinct chunks of a 128-byte line; four rows
-// read at a pair of chunks (the V^T fragments) on four distinct pairs. The
-// swizzle stays inside 128-byte lines and is its own inverse.
+// Physical 16-byte chunk of logical chunk c in row r. LDS serves a 16-byte
+// read for 16 lanes per pass from 64 banks (256 bytes), and K / V rows of
+// D >= 128 are 256 or 512 bytes long, so every row starts at bank 0. With
+// 16 or more chunks per row the low four chunk bits XOR h(r % 16) = f(r % 8)
+// + (r & 8), f = 0 2 4 6 1 3 5 7: the 16 rows one K fragment read touches
+// per pass (lanes 0-15: rows 0-15 at one logical chunk) land on 16 distinct
+// chunks of a 256-byte window, and the four rows each 16-lane group of a
+// transposed V^T read touches (two chunks each) on eight distinct chunks.
+// Rows of D = 64 (128 bytes, 8 chunks) XOR f(r % 8) in the low three bits.
+// The swizzle is its own inverse.
 __host__ __device__ constexpr int swz_f(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
-__host__ __device__ constexpr int swz(int r, int c) { return (c & ~7) | ((c & 7) ^ swz_f(r & 7)); }
+template <int D> __host__ __device__ constexpr int swz(int r, int c)
+{
+    return D >= 128 ? (c & ~15) | ((c & 15) ^ (swz_f(r & 7) | (r & 8))) : (c & ~7) | ((c & 7) ^ swz_f(r & 7));
+}
 }
 
 // LDS fragment reads of the main loop, as inline asm. The compiler's wait
@@ -127,31 +135,42 @@ __device__ __forceinline__ void fa_lgkm_wait()
 
 __device__ __forceinline__ void fa_pin(half8& v) { asm volatile("" : "+v"(v)); }
 
-// K fragment of S^T step IDX (key block IDX % 2, head-dim step s = IDX / 2):
-// lane (ql, hf) reads key row 32 (IDX % 2) + ql, head-dim values 16 s + 8 hf
-// .. +7, i.e. logical chunk 2 s + hf. With the row's swizzle f(ql % 8) the
-// lane part is kaddr[s % 4] = stage + ql ROWB + ((2 (s % 4) + hf) ^ f) 16;
-// the rest is the immediate 32 (IDX % 2) ROWB + (s / 4) 128.
+// K fragment of S^T step IDX (key block IDX % 2, head-dim step S = IDX / 2):
+// lane (ql, hf) reads key row 32 (IDX % 2) + ql, head-dim values 16 S + 8 hf
+// .. +7, i.e. logical chunk c = 2 S + hf. D >= 128: the physical chunk is
+// 16 (S / 8) + (((2 (S % 4) + hf) ^ f(ql % 8)) | (8 ((S / 4) % 2) ^ (ql & 8))),
+// so the lane part is kaddr[S % 8] = stage + ql ROWB + that chunk without its
+// first term, times 16, and the immediate adds 32 (IDX % 2) ROWB + 256 (S / 8).
+// D = 64 (S < 4): kaddr[S] with the three-bit swizzle.
+template <int D>
+constexpr int fa_nk = D >= 128 ? 8 : 4;
 template <int D, int IDX>
-__device__ __forceinline__ half8 fa_kfrag(const uint32_t (&kaddr)[4])
+__device__ __forceinline__ half8 fa_kfrag(const uint32_t (&kaddr)[fa_nk<D>])
 {
     constexpr int S = IDX >> 1;
-    return lds_read128<32 * (IDX & 1) * fa::Lds<D>::ROWB + (S >> 2) * 128>(kaddr[S & 3]);
+    return lds_read128<32 * (IDX & 1) * fa::Lds<D>::ROWB + (S >> 3) * 256>(kaddr[S & (fa_nk<D> - 1)]);
 }
 
 // V^T fragment of key step KK, head-dim block DD: two transposed 8-byte reads
-// of keys 16 KK + 8 part + vkey + vrow, head-dim values 32 DD + vcol .. +3
-// (logical chunk 4 DD + vcol / 8). The lane part is vaddr[DD % 2] = stage +
-// TILE-relative row (vkey + vrow) ROWB + ((4 (DD % 2) + vcol / 8) ^ f) 16 +
-// (vcol % 8) 2; the immediate adds the V tile, (16 KK + 8 part) ROWB and
-// (DD / 2) 128.
+// of keys 16 KK + 8 part + lr (lr = vkey + vrow < 8), head-dim values 32 DD +
+// vcol .. +3 (logical chunk c = 4 DD + vcol / 8). The row's swizzle is f(lr)
+// plus 8 part, so the physical chunk is 16 (DD / 4) + ((4 (DD % 2) + vcol / 8)
+// ^ f(lr)) + 8 ((DD / 2) % 2 ^ part) (D = 64: DD < 2, no bit 3). The lane part
+// is vaddr[DD % 2] = stage + lr ROWB + ((4 (DD % 2) + vcol / 8) ^ f(lr)) 16 +
+// (vcol % 8) 2; the immediate adds the V tile, (16 KK + 8 part) ROWB and the
+// rest of the chunk.
+template <int D, int KK, int DD, int PART>
+constexpr int fa_voff()
+{
+    using L = fa::Lds<D>;
+    return L::TILE + (16 * KK + 8 * PART) * L::ROWB + (DD >> 2) * 256 +
+           (D >= 128 ? (((DD >> 1) & 1) ^ PART) * 128 : (DD >> 1) * 128);
+}
 template <int D, int KK, int DD>
 __device__ __forceinline__ half8 fa_vfrag(const uint32_t (&vaddr)[2])
 {
-    using L = fa::Lds<D>;
-    constexpr int base = L::TILE + 16 * KK * L::ROWB + (DD >> 1) * 128;
-    const half4 h0 = lds_read_tr16<base>(vaddr[DD & 1]);
-    const half4 h1 = lds_read_tr16<base + 8 * L::ROWB>(vaddr[DD & 1]);
+    const half4 h0 = lds_read_tr16<fa_voff<D, KK, DD, 0>()>(vaddr[DD & 1]);
+    const half4 h1 = lds_read_tr16<fa_voff<D, KK, DD, 1>()>(vaddr[DD & 1]);
     return __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
@@ -289,7 +308,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 
     // K / V tile copies: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
     // lane l's 16 bytes land at physical chunk pc of row r and come from
-    // logical chunk swz(r, pc) of that row (the swizzle is its own inverse).
+    // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D), (short)0, (int)((size_t)Tkv * D * 2),
         0x00020000);
@@ -301,7 +320,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     for (int j = 0; j < L::COPIES; ++j) {
         const int byte = (wave * L::COPIES + j) * 1024 + lane * 16;
         const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16;
-        coff[j] = (uint32_t)(r * L::ROWB + swz(r, pc) * 16);
+        coff[j] = (uint32_t)(r * L::ROWB + swz<D>(r, pc) * 16);
     }
     const auto issue = [&](int t) __attribute__((always_inline)) {
         fa_issue<D>(rk, rv, lds, coff, (int)(tb + t) * BKV, t, wave);
@@ -323,9 +342,12 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     const int vkey = 4 * (g >> 1);
     // lane parts of the fragment addresses (fa_kfrag, fa_vfrag), stage 0
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
-    uint32_t kofs[4], vofs[2];
+    constexpr int NK = fa_nk<D>;
+    uint32_t kofs[NK], vofs[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kofs[j] = lds0 + ql * L::ROWB + ((2 * j + hf) ^ swz_f(ql & 7)) * 16;
+    for (int j = 0; j < NK; ++j)
+        kofs[j] = lds0 + ql * L::ROWB +
+                  (((2 * (j & 3) + hf) ^ swz_f(ql & 7)) + (D >= 128 ? (8 * (j >> 2)) ^ (ql & 8) : 0)) * 16;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
         vofs[j] = lds0 + (vkey + vrow) * L::ROWB + ((4 * j + (vcol >> 3)) ^ swz_f((vkey + vrow) & 7)) * 16 +
@@ -347,7 +369,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         const int row = wave * QW + ql, rr = row % BKV;
         LDS_AS const char* qs = lds + L::STAGE + (row / BKV) * L::TILE + rr * L::ROWB;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) qf[s] = *(LDS_AS const half8*)(qs + swz(rr, 2 * s + hf) * 16);
+        for (int s = 0; s < KS; ++s) qf[s] = *(LDS_AS const half8*)(qs + swz<D>(rr, 2 * s + hf) * 16);
     }
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
@@ -360,9 +382,9 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         }
         __builtin_amdgcn_s_barrier();
         const uint32_t sb = (t & 1) * L::STAGE;
-        uint32_t kaddr[4], vaddr[2];
+        uint32_t kaddr[NK], vaddr[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kaddr[j] = kofs[j] + sb;
+        for (int j = 0; j < NK; ++j) kaddr[j] = kofs[j] + sb;
 #pragma unroll
         for (int j = 0; j < 2; ++j) vaddr[j] = vofs[j] + sb;
         const int64_t j0 = (tb + t) * BKV;

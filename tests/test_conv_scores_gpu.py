@@ -99,6 +99,42 @@ def test_config5_yolox_conv(gpu):
     assert_close(got, want, TRANS)
 
 
+@pytest.mark.parametrize("ci, co, hi, wi, batch, epi", [
+    (40, 48, 16, 16, 2, "SILU"),      # channels and output channels past a block, batch 2
+    (64, 32, 20, 32, 1, "RELU"),      # two column fragments, H != W
+    (160, 32, 9, 48, 1, "SIGMOID"),   # five channel blocks: a wave takes two
+    (128, 64, 6, 128, 1, "NONE"),     # eight column fragments (the widest row)
+    (3, 16, 5, 16, 1, "GELU"),        # three input channels
+])
+def test_conv3_lds_transpose(gpu, ci, co, hi, wi, batch, epi):
+    """The 3x3 stride-1 plan for fp16 rows of 16 NF columns (input copied to
+    LDS as NCHW, transposed by the LDS read, kw taps combined by a column
+    shift): borders, channel and output-channel tails, several channel
+    blocks per wave, one to eight column fragments."""
+    rng = np.random.default_rng(ci + wi)
+    w = draw(normal((co, ci, 3, 3), 1.0 / np.sqrt(ci * 9)), rng, np.float16)
+    b = draw(normal((co,), 0.1), rng, np.float16)
+    x = draw((batch, ci, hi, wi), rng, np.float16)
+    print(f"conv3 ci={ci} co={co} hi={hi} wi={wi} batch={batch}", flush=True)
+    got = run_conv(gpu, x, w, b, epi=epi)
+    assert_close(got, oracle.conv2d(x, w, b, epi=epi), FP16)
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_conv3_lds_transpose_scale_residual(gpu, order):
+    """Scale, fp16 residual (both orders) and fp16 output on the same plan."""
+    rng = np.random.default_rng(order)
+    ci, co, hw = 32, 32, 32
+    w = draw(normal((co, ci, 3, 3), 0.1), rng, np.float16)
+    b = draw((co,), rng, np.float16)
+    s = draw(uniform((co,), 0.5, 1.5), rng, np.float16)
+    x = draw((1, ci, hw, hw), rng, np.float16)
+    r = draw((1, co, hw, hw), rng, np.float16)
+    got = run_conv(gpu, x, w, b, s, r, out_dtype=np.float16, epi="RELU", order=order).astype(np.float32)
+    want = oracle.conv2d(x, w, b, s, r, epi="RELU", order=order)
+    assert_close(got, want, FP16)
+
+
 def run_scores(capi, q, k, **kw):
     dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
     out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)

@@ -82,6 +82,96 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(half_t* __restrict__ d
     }
 }
 
+// Scale, bias, residual and activation of a workgroup's 32 output channels x
+// one output row, from the partial sums of its four channel-block waves in
+// LDS (red[w][32][rw], positions along a row), with stores per output row.
+// 512 threads.
+__device__ __forceinline__ void conv_store(const ConvParams& p, const float* red, uint32_t rw, const float* epi_bs,
+                                           uint32_t co0, uint32_t ho, uint32_t b)
+{
+    using namespace cv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int EPI_COLS = CO_TILE / 8;   // output channels per wave in the scalar path
+    const size_t HoWo = (size_t)p.ho * p.wo;
+    const bool vec4 = p.wo % 4 == 0 && (uintptr_t)p.out % 16 == 0 && (uintptr_t)p.residual % 16 == 0;
+    if (vec4) {
+        // 4 consecutive positions of one output channel per work item: four
+        // 16-byte partial-sum reads, one 16-byte (fp32) or 8-byte (fp16)
+        // store. A row of Wo outputs stays 16-byte aligned (Ho Wo and Wo
+        // are multiples of 4).
+        const uint32_t q4 = p.wo / 4, items = CO_TILE * q4;
+        for (uint32_t it = tid; it < items; it += 512) {
+            const uint32_t col = it / q4, wo = (it % q4) * 4, co = co0 + col;
+            if (co >= p.co) continue;
+            float4v v = *(const float4v*)(red + (size_t)col * rw + wo);
+#pragma unroll
+            for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CO_TILE + col) * rw + wo);
+            const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
+            const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
+            float4v rr = (float4v)0.f;
+            if (p.residual) {
+                if (p.residual_dtype == DT_F16) rr = __builtin_convertvector(*(const half4*)((const half_t*)p.residual + o), float4v);
+                else rr = *(const float4v*)((const float*)p.residual + o);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x = p.scale ? fmaf(v[e], sc, bias) : v[e] + bias;
+                if (p.residual && p.residual_order == 1) x += rr[e];
+                x = epilogue(x, p.epilogue);
+                if (p.residual && p.residual_order == 0) x += rr[e];
+                v[e] = x;
+            }
+            if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(v, half4);
+            else *(float4v*)((float*)p.out + o) = v;
+        }
+        return;
+    }
+    // Outputs (co0 + wave + 8 i, wo = lane + 64 k); residuals first, all
+    // loads in flight together (indices clamped, unused values discarded).
+    constexpr int EPI_W = MAX_WO_FRAGS * 16 / 64;
+    float rv[EPI_COLS][EPI_W] = {};
+    if (p.residual) {
+        const bool r16 = p.residual_dtype == DT_F16;
+#pragma unroll
+        for (int i = 0; i < EPI_COLS; ++i)
+#pragma unroll
+            for (int k = 0; k < EPI_W; ++k) {
+                const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
+                const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
+                rv[i][k] = r16 ? (float)((const half_t*)p.residual)[o] : 0.f;
+            }
+        if (!r16) {
+#pragma unroll
+            for (int i = 0; i < EPI_COLS; ++i)
+#pragma unroll
+                for (int k = 0; k < EPI_W; ++k) {
+                    const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
+                    rv[i][k] = ((const float*)p.residual)[((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo];
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPI_COLS; ++i) {
+        const uint32_t col = wave + 8 * i, co = co0 + col;
+        if (co >= p.co) break;
+        const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
+        const size_t obase = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo;
+#pragma unroll
+        for (int k = 0; k < EPI_W; ++k) {
+            const uint32_t wo = lane + 64 * k;
+            if (wo >= p.wo) break;
+            float v = red[(size_t)col * rw + wo] + red[((size_t)CO_TILE + col) * rw + wo] +
+                      red[((size_t)2 * CO_TILE + col) * rw + wo] + red[((size_t)3 * CO_TILE + col) * rw + wo];
+            v = p.scale ? fmaf(v, sc, bias) : v + bias;
+            const float rr = rv[i][k];
+            if (p.residual && p.residual_order == 1) v += rr;
+            v = epilogue(v, p.epilogue);
+            if (p.residual && p.residual_order == 0) v += rr;
+            st(p.out, p.o_dtype, obase + wo, v);
+        }
+    }
+}
+
 template <int KS, int NF, typename TI>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void conv_kernel(ConvParams p)
 {
@@ -108,7 +198,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
             wa[tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * nblk + cb) * 64 + lane) * 8);
     };
     if ((uint32_t)cw < nblk) load_w(cw);
-    constexpr int EPI_COLS = CO_TILE / 8;   // output channels per wave in the epilogue
 
     // ---- input rows: NCHW -> LDS [row][pad + w][c] ----
     // Work item = 8 channels x 8 columns of one input row: eight 16-byte
@@ -232,84 +321,241 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
             for (int r = 0; r < 4; ++r)
                 red[((size_t)cw * CO_TILE + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
     __syncthreads();
-    const size_t HoWo = (size_t)p.ho * p.wo;
-    const bool vec4 = p.wo % 4 == 0 && (uintptr_t)p.out % 16 == 0 && (uintptr_t)p.residual % 16 == 0;
-    if (vec4) {
-        // 4 consecutive positions of one output channel per work item: four
-        // 16-byte partial-sum reads, one 16-byte (fp32) or 8-byte (fp16)
-        // store. A row of Wo outputs stays 16-byte aligned (Ho Wo and Wo
-        // are multiples of 4).
-        const uint32_t q4 = p.wo / 4, items = CO_TILE * q4;
-        for (uint32_t it = tid; it < items; it += 512) {
-            const uint32_t col = it / q4, wo = (it % q4) * 4, co = co0 + col;
-            if (co >= p.co) continue;
-            float4v v = *(const float4v*)(red + (size_t)col * rw + wo);
-#pragma unroll
-            for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CO_TILE + col) * rw + wo);
-            const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
-            const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
-            float4v rr = (float4v)0.f;
-            if (p.residual) {
-                if (p.residual_dtype == DT_F16) rr = __builtin_convertvector(*(const half4*)((const half_t*)p.residual + o), float4v);
-                else rr = *(const float4v*)((const float*)p.residual + o);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float x = p.scale ? fmaf(v[e], sc, bias) : v[e] + bias;
-                if (p.residual && p.residual_order == 1) x += rr[e];
-                x = epilogue(x, p.epilogue);
-                if (p.residual && p.residual_order == 0) x += rr[e];
-                v[e] = x;
-            }
-            if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(v, half4);
-            else *(float4v*)((float*)p.out + o) = v;
-        }
-        return;
+    conv_store(p, red, rw, epi_bs, co0, ho, b);
+}
+
+// ---- 3x3, stride 1, fp16 NCHW input, row width 16 NF (config 5's shape) ----
+// The input rows go global -> LDS unchanged, by buffer_load ... lds (each
+// channel's rows are contiguous halves in NCHW as in LDS), and the transpose
+// to channel-major MFMA operands happens in the LDS read: ds_read_b64_tr_b16
+// gives lane j of a 16-lane group 4 consecutive channels of column j, where
+// source lane 4 k + q points at channel k, columns 4 q .. +3 (two reads: the
+// lane's 8 channels). A B fragment (32 channels x 16 columns, unshifted)
+// serves all three kw taps: tap kw accumulates into its own P_kw, and the
+// taps meet at the end shifted by one column,
+//   out(x) = P_0(x - 1) + P_1(x) + P_2(x + 1),
+// the shift a DPP row rotation (a fragment's 16 columns are the 16 lanes of
+// a row) with the edge column taken from the neighbouring fragment, zero at
+// the image border (the padding). This replaces the VALU transpose of the
+// general kernel's staging.
+//
+// A workgroup covers 32 output channels x one output row with 8 waves
+// (channel block lane, output-channel half), as the general kernel. (Two
+// rows per workgroup, with the weight fragments copied into LDS once for
+// both, halve the bytes per row but leave 96 of the 256 CUs idle at config
+// 5: 9.1 against 8.3 us.)
+__host__ __device__ constexpr uint32_t conv3_stage_bytes(uint32_t c32, uint32_t nf) { return c32 * 96 * nf; }
+__host__ __device__ inline size_t conv3_main_lds_bytes(uint32_t c32, uint32_t nf)
+{
+    const size_t red = 4ull * cv::CO_TILE * 16 * nf * 4;
+    return conv3_stage_bytes(c32, nf) > red ? conv3_stage_bytes(c32, nf) : red;
+}
+__host__ __device__ inline size_t conv3_lds_bytes(uint32_t c32, uint32_t nf)
+{
+    return conv3_main_lds_bytes(c32, nf) + 2 * cv::CO_TILE * sizeof(float);
+}
+
+// The C32 channels x 3 rows x WI columns of image b around output row ho
+// into LDS, in 1 KB copies per wave instruction: byte pos of the stage is
+// channel pos / CHB, row (pos % CHB) / ROWB, column bytes the rest. Rows
+// outside the image and channels past Ci read as zero (offset 2^31, or past
+// the resource's end).
+template <int NF>
+__device__ __forceinline__ void conv3_stage(const ConvParams& p, __attribute__((address_space(3))) char* xs,
+                                            uint32_t c32, uint32_t ho, uint32_t b, int wave, int lane)
+{
+    constexpr uint32_t ROWB = 32 * NF, CHB = 3 * ROWB, NW = 8;
+    const uint32_t plane_bytes = p.hi * ROWB;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const half_t*)p.x + (size_t)b * p.ci * p.hi * (16 * NF)), (short)0, (int)(p.ci * plane_bytes),
+        0x00020000);
+    const uint32_t n = c32 * CHB;
+    for (uint32_t i0 = (uint32_t)wave * 1024; i0 < n; i0 += NW * 1024) {
+        const uint32_t pos = i0 + (uint32_t)lane * 16, c = pos / CHB, w = pos % CHB, r = w / ROWB;
+        const int hi = (int)ho + (int)r - 1;
+        const uint32_t off = (hi >= 0 && hi < (int)p.hi) ? c * plane_bytes + (uint32_t)hi * ROWB + w % ROWB
+                                                          : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(xs + i0), 16, (int)off,
+                                                 0, 0, 0);
     }
-    // Outputs (co0 + wave + 8 i, wo = lane + 64 k); residuals first, all
-    // loads in flight together (indices clamped, unused values discarded).
-    constexpr int EPI_W = MAX_WO_FRAGS * 16 / 64;
-    float rv[EPI_COLS][EPI_W] = {};
-    if (p.residual) {
-        const bool r16 = p.residual_dtype == DT_F16;
+}
+
+typedef __fp16 cv_fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+__device__ __forceinline__ half4 cv_read_tr16(const __attribute__((address_space(3))) char* a)
+{
+    return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                         (__attribute__((address_space(3))) cv_fp16x4*)a));
+}
+
+// x of lane (j - 1) of its 16-lane row (k = 1), or of lane (j + 1) (k = 15).
+template <int K>
+__device__ __forceinline__ float cv_row_ror(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + K, 0xF, 0xF,
+                                                                 false));
+}
+
+// The epilogue: 8 consecutive positions of one output channel per thread
+// (32 x 2 NF items, one pass): the residual loads first, then the four
+// partial sums from LDS, scale and bias, the activation chosen once per
+// thread (EPI), and one 32-byte (fp32) or 16-byte (fp16) store.
+template <int EPI>
+__device__ __forceinline__ float cv_act(float x)
+{
+    if constexpr (EPI == 1) return x > 0.f ? x : 0.f;
+    else if constexpr (EPI == 2) return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
+    else if constexpr (EPI == 3) return 0.5f * x * (1.0f + fast_tanh(0.79788456080286535f * (x + 0.044715f * x * x * x)));
+    else if constexpr (EPI == 4) return x * fast_rcp(1.0f + fast_exp(-x));
+    else if constexpr (EPI == 5) return fast_rcp(1.0f + fast_exp(-x));
+    else return x;
+}
+
+template <int EPI>
+__device__ __forceinline__ void cv_finish8(float8v& v, const float8v& rr, bool res, uint32_t order, float sc, float bias,
+                                           bool scaled)
+{
 #pragma unroll
-        for (int i = 0; i < EPI_COLS; ++i)
+    for (int e = 0; e < 8; ++e) {
+        float x = scaled ? fmaf(v[e], sc, bias) : v[e] + bias;
+        if (res && order == 1) x += rr[e];
+        x = cv_act<EPI>(x);
+        if (res && order == 0) x += rr[e];
+        v[e] = x;
+    }
+}
+
+template <int NF>
+__device__ __forceinline__ void conv3_store(const ConvParams& p, const float* red, const float* epi_bs, uint32_t co0,
+                                            uint32_t ho, uint32_t b)
+{
+    constexpr uint32_t RW = NF * 16, Q8 = 2 * NF;
+    const uint32_t it = threadIdx.x;
+    if (it >= cv::CO_TILE * Q8) return;
+    const uint32_t col = it / Q8, wo = (it % Q8) * 8, co = co0 + col;
+    if (co >= p.co) return;
+    const size_t o = ((size_t)b * p.co + co) * ((size_t)p.ho * RW) + (size_t)ho * RW + wo;
+    const bool res = p.residual != nullptr;
+    float8v rr = (float8v)0.f;
+    if (res) {
+        if (p.residual_dtype == DT_F16) rr = __builtin_convertvector(*(const half8*)((const half_t*)p.residual + o), float8v);
+        else rr = *(const float8v*)((const float*)p.residual + o);
+    }
+    const float* rp = red + (size_t)col * RW + wo;
+    float8v v = *(const float8v*)rp;
 #pragma unroll
-            for (int k = 0; k < EPI_W; ++k) {
-                const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
-                const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
-                rv[i][k] = r16 ? (float)((const half_t*)p.residual)[o] : 0.f;
+    for (int w = 1; w < 4; ++w) v += *(const float8v*)(rp + (size_t)w * cv::CO_TILE * RW);
+    const float bias = p.bias ? epi_bs[col] : 0.f, sc = epi_bs[cv::CO_TILE + col];
+    const bool scaled = p.scale != nullptr;
+    switch (p.epilogue) {
+    case 1: cv_finish8<1>(v, rr, res, p.residual_order, sc, bias, scaled); break;
+    case 2: cv_finish8<2>(v, rr, res, p.residual_order, sc, bias, scaled); break;
+    case 3: cv_finish8<3>(v, rr, res, p.residual_order, sc, bias, scaled); break;
+    case 4: cv_finish8<4>(v, rr, res, p.residual_order, sc, bias, scaled); break;
+    case 5: cv_finish8<5>(v, rr, res, p.residual_order, sc, bias, scaled); break;
+    default: cv_finish8<0>(v, rr, res, p.residual_order, sc, bias, scaled); break;
+    }
+    if (p.o_dtype == DT_F16) *(half8*)((half_t*)p.out + o) = __builtin_convertvector(v, half8);
+    else *(float8v*)((float*)p.out + o) = v;
+}
+
+template <int NF>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void conv3_tr_kernel(ConvParams p)
+{
+    using namespace cv;
+    constexpr uint32_t ROWB = 32 * NF, CHB = 3 * ROWB;
+    extern __shared__ half8 smem[];
+    __attribute__((address_space(3))) char* xs = (__attribute__((address_space(3))) char*)(
+        __attribute__((address_space(3))) void*)smem;
+    const uint32_t C32 = ci32(p.ci), nblk = C32 / 32;
+    float* epi_bs = (float*)((char*)smem + conv3_main_lds_bytes(C32, NF));   // [bias x 32, scale x 32]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cw = wave & 3, half = wave >> 2;   // channel-block lane, output-channel half
+    const uint32_t co0 = blockIdx.x * CO_TILE, ho = blockIdx.y, b = blockIdx.z;
+    const int fr = lane & 15, fg = lane >> 4;
+
+    // the nine taps' A fragments of channel block cb (issued before the staging)
+    half8 wa[9];
+    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * 2 + half, CO16 - 1);   // past Co: discarded
+    auto load_w = [&](uint32_t cb) {
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+            wa[tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * nblk + cb) * 64 + lane) * 8);
+    };
+    if ((uint32_t)cw < nblk) load_w(cw);
+    conv3_stage<NF>(p, xs, C32, ho, b, wave, lane);
+    if (tid < 2 * CO_TILE) {   // bias and scale (a missing one reads the packed weight; ignored)
+        const half_t* src = tid < CO_TILE ? (p.bias ? (const half_t*)p.bias : p.wp)
+                                          : (p.scale ? (const half_t*)p.scale : p.wp);
+        epi_bs[tid] = (float)src[min(co0 + (tid % CO_TILE), p.co - 1)];
+    }
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));   // vmcnt(0): copies landed
+    __syncthreads();
+
+    float4v P[3][NF];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) P[k][f] = (float4v)0.f;
+    for (uint32_t cb = cw; cb < nblk; cb += 4) {
+        if (cb != (uint32_t)cw) load_w(cb);
+        // source lane (k, q) = (fr / 4, fr % 4) of group fg: channel cb 32 + 8 fg + k, columns 4 q ..
+        const __attribute__((address_space(3))) char* base = xs + (cb * 32 + 8 * fg + (fr >> 2)) * CHB + (fr & 3) * 8;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const half4 lo = cv_read_tr16(base + kh * ROWB + f * 32);
+                const half4 hi = cv_read_tr16(base + 4 * CHB + kh * ROWB + f * 32);
+                const half8 bv = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw)
+                    P[kw][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[kh * 3 + kw], bv, P[kw][f], 0, 0, 0);
             }
-        if (!r16) {
-#pragma unroll
-            for (int i = 0; i < EPI_COLS; ++i)
-#pragma unroll
-                for (int k = 0; k < EPI_W; ++k) {
-                    const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
-                    rv[i][k] = ((const float*)p.residual)[((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo];
-                }
-        }
     }
+    // the taps combined: column j of fragment f is lane fr = j of each row
+    float4v acc[NF];
 #pragma unroll
-    for (int i = 0; i < EPI_COLS; ++i) {
-        const uint32_t col = wave + 8 * i, co = co0 + col;
-        if (co >= p.co) break;
-        const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
-        const size_t obase = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo;
+    for (int f = 0; f < NF; ++f)
 #pragma unroll
-        for (int k = 0; k < EPI_W; ++k) {
-            const uint32_t wo = lane + 64 * k;
-            if (wo >= p.wo) break;
-            float v = red[(size_t)col * rw + wo] + red[((size_t)CO_TILE + col) * rw + wo] +
-                      red[((size_t)2 * CO_TILE + col) * rw + wo] + red[((size_t)3 * CO_TILE + col) * rw + wo];
-            v = p.scale ? fmaf(v, sc, bias) : v + bias;
-            const float rr = rv[i][k];
-            if (p.residual && p.residual_order == 1) v += rr;
-            v = epilogue(v, p.epilogue);
-            if (p.residual && p.residual_order == 0) v += rr;
-            st(p.out, p.o_dtype, obase + wo, v);
+        for (int r = 0; r < 4; ++r) {
+            const float a0 = cv_row_ror<1>(P[0][f][r]);
+            const float e0 = f > 0 ? cv_row_ror<1>(P[0][f > 0 ? f - 1 : 0][r]) : 0.f;
+            const float a2 = cv_row_ror<15>(P[2][f][r]);
+            const float e2 = f + 1 < NF ? cv_row_ror<15>(P[2][f + 1 < NF ? f + 1 : f][r]) : 0.f;
+            acc[f][r] = P[1][f][r] + (fr == 0 ? e0 : a0) + (fr == 15 ? e2 : a2);
         }
-    }
+    __syncthreads();   // every wave done reading the stage before the sums overwrite it
+    float* red = (float*)smem;   // [4 channel lanes][32 co][16 NF positions]
+    constexpr uint32_t rw = NF * 16;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((size_t)cw * CO_TILE + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
+    __syncthreads();
+    conv3_store<NF>(p, red, epi_bs, co0, ho, b);
+}
+
+// Whether the 3x3 LDS-transpose plan applies: fp16 NCHW rows of 16 NF
+// columns (NF <= 8), stride 1, aligned buffers, and the stage fits LDS.
+bool conv3_tr_ok(const ConvParams& p, int x_dt)
+{
+    const uint32_t nf = p.wi / 16;
+    return p.ks == 3 && p.stride == 1 && x_dt == DT_F16 && p.wi % 16 == 0 && nf >= 1 && nf <= 8 && p.wo == p.wi &&
+           p.ho == p.hi && ((uintptr_t)p.x % 16) == 0 && ((uintptr_t)p.out % 32) == 0 &&
+           ((uintptr_t)p.residual % 32) == 0 && (size_t)p.ci * p.hi * p.wi * 2 < (1ull << 31) &&
+           conv3_lds_bytes(cv::ci32(p.ci), nf) <= 160u * 1024u;
+}
+
+template <int NF>
+static hipError_t launch_tr(const ConvParams& p, hipStream_t s)
+{
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)conv3_tr_kernel<NF>, 160 * 1024);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(conv3_tr_kernel<NF>, dim3((p.co + cv::CO_TILE - 1) / cv::CO_TILE, p.ho, p.batch), dim3(512),
+                       conv3_lds_bytes(cv::ci32(p.ci), NF), s, p);
+    return hipGetLastError();
 }
 
 size_t conv_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks)
@@ -363,6 +609,18 @@ static hipError_t launch_ks(const ConvParams& p, int x_dt, size_t lds, hipStream
 
 hipError_t conv_launch(const ConvParams& p, int x_dt, hipStream_t s)
 {
+    if (conv3_tr_ok(p, x_dt)) {
+        switch (p.wi / 16) {
+        case 1: return launch_tr<1>(p, s);
+        case 2: return launch_tr<2>(p, s);
+        case 3: return launch_tr<3>(p, s);
+        case 4: return launch_tr<4>(p, s);
+        case 5: return launch_tr<5>(p, s);
+        case 6: return launch_tr<6>(p, s);
+        case 7: return launch_tr<7>(p, s);
+        default: return launch_tr<8>(p, s);
+        }
+    }
     const size_t lds = conv_lds_bytes(p.ci, p.wi, p.ks);
     return p.ks == 1 ? launch_ks<1>(p, x_dt, lds, s) : launch_ks<3>(p, x_dt, lds, s);
 }

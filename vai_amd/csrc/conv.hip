@@ -209,8 +209,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
     {
         const uint32_t ngc = C32 / 8, ngw = (p.wi + 7) / 8, items = KS * ngc * ngw;
         const size_t plane = (size_t)p.hi * p.wi;
+        // (channel offsets up to C32 planes, plus 2^31 for a row outside the
+        // image, must stay 32-bit and past the resource's end)
         const bool vec = p.wi % 8 == 0 && ((uintptr_t)p.x % (8 * sizeof(TI))) == 0 &&
-                         (size_t)p.ci * plane * sizeof(TI) < (1ull << 31);
+                         (size_t)C32 * plane * sizeof(TI) < (1ull << 31);
         const uint32_t plane_bytes = (uint32_t)(plane * sizeof(TI));
         const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void*)((const TI*)p.x + (size_t)b * p.ci * plane), (short)0,
@@ -359,7 +361,7 @@ __host__ __device__ inline size_t conv3_lds_bytes(uint32_t c32, uint32_t nf)
 // into LDS, in 1 KB copies per wave instruction: byte pos of the stage is
 // channel pos / CHB, row (pos % CHB) / ROWB, column bytes the rest. Rows
 // outside the image and channels past Ci read as zero (offset 2^31, or past
-// the resource's end).
+// the resource's end; C32 planes stay under 2^31 bytes, so no offset wraps).
 template <int NF>
 __device__ __forceinline__ void conv3_stage(const ConvParams& p, __attribute__((address_space(3))) char* xs,
                                             uint32_t c32, uint32_t ho, uint32_t b, int wave, int lane)
@@ -543,7 +545,7 @@ bool conv3_tr_ok(const ConvParams& p, int x_dt)
     const uint32_t nf = p.wi / 16;
     return p.ks == 3 && p.stride == 1 && x_dt == DT_F16 && p.wi % 16 == 0 && nf >= 1 && nf <= 8 && p.wo == p.wi &&
            p.ho == p.hi && ((uintptr_t)p.x % 16) == 0 && ((uintptr_t)p.out % 32) == 0 &&
-           ((uintptr_t)p.residual % 32) == 0 && (size_t)p.ci * p.hi * p.wi * 2 < (1ull << 31) &&
+           ((uintptr_t)p.residual % 32) == 0 && (size_t)cv::ci32(p.ci) * p.hi * p.wi * 2 < (1ull << 31) &&
            conv3_lds_bytes(cv::ci32(p.ci), nf) <= 160u * 1024u;
 }
 

@@ -25,6 +25,8 @@ pytestmark = pytest.mark.gpu
     (1, 1, 1, 70, 40, 64, True, 0, np.float32),          # Tq > Tkv: the first 30 queries see no key
     (1, 2, 2, 64, 1000, 128, False, 0, np.float32),      # one query tile, 16 key tiles: split in 4 and merged
     (1, 2, 2, 600, 520, 64, True, 0, np.float16),        # split, and a query tile that sees no key
+    (1, 2, 2, 64, 4096, 64, False, 0, np.float16),       # 32 chunks per query tile: the merge's general path
+    (1, 1, 1, 2176, 2176, 64, True, 0, np.float16),      # 17 query tiles: the merge reads the unit table
 ])
 def test_attention(gpu, b, hq, hkv, tq, tkv, d, causal, span, odt):
     rng = np.random.default_rng(7)

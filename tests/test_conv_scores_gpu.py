@@ -135,6 +135,48 @@ def test_conv3_lds_transpose_scale_residual(gpu, order):
     assert_close(got, want, FP16)
 
 
+class _Offset:
+    """A buffer `off` bytes into a larger DeviceArray (to miss an alignment on purpose)."""
+
+    def __init__(self, gpu, shape, dtype, off, data=None):
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self._base = gpu.DeviceArray((self.nbytes + off,), np.uint8)
+        self.ptr = self._base.ptr + off
+        self.code = gpu.dtype_code(self.dtype)
+        self._lib = gpu.lib()
+        if data is not None:
+            a = np.ascontiguousarray(data, self.dtype)
+            gpu.check(self._lib.vai_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes, None), "h2d")
+
+    def numpy(self):
+        import ctypes
+        out = np.empty(self.shape, self.dtype)
+        self._lib.vai_memcpy_d2h(ctypes.c_void_p(out.ctypes.data), ctypes.c_void_p(self.ptr),
+                                 ctypes.c_size_t(self.nbytes), None)
+        return out
+
+
+@pytest.mark.parametrize("off", [0, 16])
+def test_conv3_output_alignment(gpu, off):
+    """An output and residual 16 bytes past a 32-byte boundary leave the
+    LDS-transpose plan (its 8-wide stores need 32-byte alignment) for the
+    general kernel; both placements give the oracle's result."""
+    rng = np.random.default_rng(11)
+    ci, co, hw = 32, 32, 32
+    w = draw(normal((co, ci, 3, 3), 0.1), rng, np.float16)
+    b = draw((co,), rng, np.float16)
+    x = draw((1, ci, hw, hw), rng, np.float16)
+    r = draw((1, co, hw, hw), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    out = _Offset(gpu, (1, co, hw, hw), np.float32, off)
+    res = _Offset(gpu, (1, co, hw, hw), np.float16, off, r)
+    print(f"conv3 output offset {off}", flush=True)
+    gpu.conv2d(out, D(x), D(w), D(b), None, res, epi="SILU", order=0)
+    assert_close(out.numpy(), oracle.conv2d(x, w, b, None, r, epi="SILU", order=0), FP16)
+
+
 def run_scores(capi, q, k, **kw):
     dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
     out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)

@@ -4,7 +4,8 @@
 //
 // The work is bound by writing S (4 bytes per score against ~2 flop/byte of
 // MFMA work per head-dim element), so the kernel is built around the store:
-//  * one workgroup per 128x128 tile (64x64 when a mask applies) of one head;
+//  * one workgroup per 128x128 tile (64x64 when a mask applies) of one head,
+//    each head's tiles on one XCD when the heads come in multiples of 8;
 //    tiles the mask hides entirely are written as -inf and never touch Q, K
 //    or the matrix cores;
 //  * Q and K rows are copied global->LDS (buffer_load ... lds) in 64-wide
@@ -60,7 +61,18 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParam
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1, fr = lane & 31, fk = lane >> 5;
-    const uint32_t m0 = blockIdx.y * T, n0 = blockIdx.x * T, bz = blockIdx.z;
+    // Workgroup w runs on XCD w % 8. With a multiple of 8 batch entries
+    // (heads), entry z's tiles go to XCD z % 8 only (w -> entry w % 8 of its
+    // group of 8, tile w / 8), so one head's Q and K rows stay in one L2.
+    uint32_t tx = blockIdx.x, ty = blockIdx.y, bz = blockIdx.z;
+    if (gridDim.z % 8 == 0) {
+        const uint32_t nt = gridDim.x * gridDim.y, w = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const uint32_t g = w / (8 * nt), r = w % (8 * nt), tile = r / 8;
+        bz = g * 8 + r % 8;
+        tx = tile % gridDim.x;
+        ty = tile / gridDim.x;
+    }
+    const uint32_t m0 = ty * T, n0 = tx * T;
     const uint32_t M = p.M, N = p.N, K = p.K;
     float* S = (float*)p.C + bz * p.c_batch_stride;
 

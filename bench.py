@@ -257,7 +257,7 @@ def build_cases(capi, stream, which):
         cases[key] = Case(f"YOLOX-s {ks}x{ks}/s{st} conv in[1,{ci},{hw},{hw}] W[{co},{ci},{ks},{ks}] fp16 +bias SiLU, fp32 out",
                           "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnc, f"conv_kernel<{ks}> (implicit GEMM, packed weight)",
                           flops, byts, "f16", key)
-    if "read" in which or "empty" in which:
+    if "read" in which or "empty" in which or "write" in which:
         # the ceiling for config 2: a plain read of W's 32 MiB, rotated like the
         # GEMV's W copies (vai_amd/probe/read_ceiling.hip), and an empty launch
         probe = ctypes.CDLL(os.path.join(ROOT, "vai_amd", "libvai_probe.so"))
@@ -277,6 +277,18 @@ def build_cases(capi, stream, which):
             cases[f"read/{name}"] = Case(f"plain read of 32 MiB ({g} workgroups x {t} threads, {l} x 16 B loads per lane "
                                          f"in flight), rotating {len(bufs)} buffers", "GB/s", nbytes / 1e9, "hbm",
                                          HBM_PEAK_GBS, fnr, "read_kernel (vai_amd/probe)", 0, nbytes, "f16", "read")
+        if "write" in which:
+            # the ceiling for config 4: writing S's 32 MiB, rotated the same way
+            probe.vai_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_void_p]
+            for name, (g, t, l) in WRITE_VARIANTS.items():
+                def fnw(i, g=g, t=t, l=l):
+                    capi.check(probe.vai_probe_write(bufs[i % len(bufs)].ptr, nbytes, g, t, l, stream.ptr), "write")
+                fnw.keep = [bufs, probe]
+                cases[f"write/{name}"] = Case(f"plain write of 32 MiB ({g} workgroups x {t} threads, {l} x 16 B "
+                                              f"non-temporal stores per lane), rotating {len(bufs)} buffers", "GB/s",
+                                              nbytes / 1e9, "hbm", HBM_PEAK_GBS, fnw, "write_kernel (vai_amd/probe)", 0,
+                                              nbytes, "f32", "write")
         if "empty" in which:
             for g in (1, 256, 1024):
                 def fne(i, g=g):
@@ -285,6 +297,15 @@ def build_cases(capi, stream, which):
                 cases[f"empty/{g}"] = Case(f"empty kernel, {g} workgroups of 256", "us", 0.0, "hbm", HBM_PEAK_GBS, fne,
                                            "empty_kernel (vai_amd/probe)", 0, 0, "-", "empty")
     return cases
+
+
+# plain-write variants: name -> (workgroups, threads per workgroup, stores per lane)
+WRITE_VARIANTS = {
+    "2048x256x4": (2048, 256, 4),
+    "1024x256x8": (1024, 256, 8),
+    "512x256x16": (512, 256, 16),
+    "256x1024x8": (256, 1024, 8),
+}
 
 
 # plain-read variants: name -> (workgroups, threads per workgroup, loads per lane)
@@ -463,7 +484,7 @@ def main():
         print(f"# cfg {key}: {case.name}: {ms*1e3:.2f} us/step, {rate:.1f} {case.unit}, "
               f"{100*achieved/case.peak:.1f}% of {case.bound} peak [{case.kernel}]", file=sys.stderr, flush=True)
     if not args.no_cpu:
-        for key, cb in cpu_baseline([k for k in report if not k.startswith(("read", "empty"))],
+        for key, cb in cpu_baseline([k for k in report if not k.startswith(("read", "empty", "write"))],
                                     args.cpu_seconds).items():
             report[key]["cpu_baseline"] = cb
     prim = report.get("2/M=1") or next(iter(report.values()))

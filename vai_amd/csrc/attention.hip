@@ -452,7 +452,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
                 }
             tmax = fa_tree_max(tv);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = swap_max32(tmax);
         // Lazy rescaling: the reference m of a row (the exponent offset of
         // its O and l) moves only when the row max exceeds it by more than
         // 8, and then for the whole wave at once (a uniform branch), so that
@@ -493,7 +493,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         }
         {
             const float ps = fa_tree_sum(tv);
-            l += ps + __shfl_xor(ps, 32, 64);
+            l += swap_sum<32>(ps, ps);
         }
 
         // O^T += V^T P^T over the tile's four 16-key steps, the next step's

@@ -117,4 +117,40 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
+// One butterfly exchange across lane bit O (16 or 32) in a single VALU
+// instruction, no LDS: v_permlane{16,32}_swap exchanges the O-lane halves
+// with bit O set in `a` with those with bit O clear in `b`, so afterwards the
+// two registers hold, per lane, the pair (lane, lane ^ O) of a (lanes with
+// bit O clear) or of b (lanes with bit O set); their sum is
+//   a[l] + a[l ^ O] where bit O of l is clear, b[l] + b[l ^ O] where it is set.
+//
+// Written as inline asm: the compiler's builtins for these instructions
+// return the first register twice here (the second result is lost). The
+// s_nops give the VALU writes before and the reads after the wait states the
+// compiler cannot insert around an asm block.
+template <int O>
+__device__ __forceinline__ void lane_swap(float& a, float& b)
+{
+    static_assert(O == 16 || O == 32, "row or half-wave exchange");
+    if constexpr (O == 16)
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    else
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+template <int O>
+__device__ __forceinline__ float swap_sum(float a, float b)
+{
+    lane_swap<O>(a, b);
+    return a + b;
+}
+
+// max(x[l], x[l ^ 32]) in every lane, by the same swap.
+__device__ __forceinline__ float swap_max32(float x)
+{
+    float y = x;
+    lane_swap<32>(x, y);
+    return fmaxf(x, y);
+}
+
 }   // namespace vai_dev

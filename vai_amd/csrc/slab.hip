@@ -44,7 +44,8 @@ __device__ __forceinline__ float dpp_add(float x)
 // Sum over the lane bits below LIMIT, lowest first: bits 0-3 stay inside a
 // row of 16 lanes and go through DPP (quad_perm 1032, quad_perm 2301,
 // row_half_mirror, row_mirror: after the lower bits are summed, each of
-// these pairs lanes that differ in the next bit); bits 4 and 5 use shuffles.
+// these pairs lanes that differ in the next bit); bits 4 and 5 use the
+// permlane swaps.
 template <int LIMIT>
 __device__ __forceinline__ float lane_sum_low(float x)
 {
@@ -52,8 +53,8 @@ __device__ __forceinline__ float lane_sum_low(float x)
     if constexpr (LIMIT > 2) x = dpp_add<0x4E>(x);
     if constexpr (LIMIT > 4) x = dpp_add<0x141>(x);
     if constexpr (LIMIT > 8) x = dpp_add<0x140>(x);
-    if constexpr (LIMIT > 16) x += __shfl_xor(x, 16, 64);
-    if constexpr (LIMIT > 32) x += __shfl_xor(x, 32, 64);
+    if constexpr (LIMIT > 16) x = swap_sum<16>(x, x);
+    if constexpr (LIMIT > 32) x = swap_sum<32>(x, x);
     return x;
 }
 
@@ -66,12 +67,17 @@ __device__ __forceinline__ void butterfly(float* acc, int lane)
 {
     if constexpr (CNT > 1) {
         constexpr int H = CNT / 2;
-        const bool upper = (lane & O) != 0;
+        if constexpr (O >= 16) {
 #pragma unroll
-        for (int i = 0; i < H; ++i) {
-            const float send = upper ? acc[i] : acc[i + H];
-            const float keep = upper ? acc[i + H] : acc[i];
-            acc[i] = keep + __shfl_xor(send, O, 64);
+            for (int i = 0; i < H; ++i) acc[i] = swap_sum<O>(acc[i], acc[i + H]);
+        } else {
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float send = upper ? acc[i] : acc[i + H];
+                const float keep = upper ? acc[i + H] : acc[i];
+                acc[i] = keep + __shfl_xor(send, O, 64);
+            }
         }
         butterfly<H, O / 2>(acc, lane);
     } else {

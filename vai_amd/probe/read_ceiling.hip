@@ -46,6 +46,37 @@ extern "C" int vai_probe_read(const void* src, size_t bytes, int grid, int threa
     return (int)hipGetLastError();
 }
 
+// The write counterpart: wave w stores STORES * 1 KB chunks from chunk
+// w * STORES with 16-byte non-temporal stores (the form the scores kernel's
+// hidden tiles use), the ceiling for a kernel bound by writing its output.
+template <int STORES>
+__global__ void write_kernel(float4v* __restrict__ dst, size_t chunks)
+{
+    const int lane = threadIdx.x & 63;
+    const size_t waves = (size_t)gridDim.x * (blockDim.x >> 6);
+    const float4v v = (float4v)(-1.f);
+    for (size_t w = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); w * STORES < chunks; w += waves) {
+        float4v* p = dst + w * STORES * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < STORES; ++i)
+            if (w * STORES + i < chunks) __builtin_nontemporal_store(v, p + i * 64);
+    }
+}
+
+extern "C" int vai_probe_write(void* dst, size_t bytes, int grid, int threads, int stores, hipStream_t stream)
+{
+    if (bytes % 1024 || (threads != 256 && threads != 512 && threads != 1024) || grid <= 0) return 1;
+    const size_t chunks = bytes / 1024;
+    float4v* p = (float4v*)dst;
+    switch (stores) {
+    case 4: hipLaunchKernelGGL(write_kernel<4>, dim3(grid), dim3(threads), 0, stream, p, chunks); break;
+    case 8: hipLaunchKernelGGL(write_kernel<8>, dim3(grid), dim3(threads), 0, stream, p, chunks); break;
+    case 16: hipLaunchKernelGGL(write_kernel<16>, dim3(grid), dim3(threads), 0, stream, p, chunks); break;
+    default: return 1;
+    }
+    return (int)hipGetLastError();
+}
+
 __global__ void empty_kernel(float* sink)
 {
     if (threadIdx.x == 1023) sink[0] = 0.f;

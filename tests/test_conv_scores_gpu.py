@@ -105,6 +105,8 @@ def test_config5_yolox_conv(gpu):
     (160, 32, 9, 48, 1, "SIGMOID"),   # five channel blocks: a wave takes two
     (128, 64, 6, 128, 1, "NONE"),     # eight column fragments (the widest row)
     (3, 16, 5, 16, 1, "GELU"),        # three input channels
+    (48, 80, 96, 96, 1, "SILU"),      # 64-channel workgroups (288 32-channel ones > 256 CUs), output-channel tail
+    (128, 128, 40, 80, 2, "NONE"),    # 64-channel workgroups over a batch of 2
 ])
 def test_conv3_lds_transpose(gpu, ci, co, hi, wi, batch, epi):
     """The 3x3 stride-1 plan for fp16 rows of 16 NF columns (input copied to
@@ -118,6 +120,22 @@ def test_conv3_lds_transpose(gpu, ci, co, hi, wi, batch, epi):
     print(f"conv3 ci={ci} co={co} hi={hi} wi={wi} batch={batch}", flush=True)
     got = run_conv(gpu, x, w, b, epi=epi)
     assert_close(got, oracle.conv2d(x, w, b, epi=epi), FP16)
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_conv3_wide_scale_residual(gpu, order):
+    """Scale, fp16 residual and fp16 output with 64-channel workgroups (2 x 96
+    rows x 2 channel blocks of 32 would be 384 workgroups on 256 CUs)."""
+    rng = np.random.default_rng(10 + order)
+    ci, co, hw = 32, 64, 96
+    w = draw(normal((co, ci, 3, 3), 0.1), rng, np.float16)
+    b = draw((co,), rng, np.float16)
+    s = draw(uniform((co,), 0.5, 1.5), rng, np.float16)
+    x = draw((2, ci, hw, hw), rng, np.float16)
+    r = draw((2, co, hw, hw), rng, np.float16)
+    got = run_conv(gpu, x, w, b, s, r, out_dtype=np.float16, epi="SILU", order=order).astype(np.float32)
+    want = oracle.conv2d(x, w, b, s, r, epi="SILU", order=order)
+    assert_close(got, want, FP16)
 
 
 @pytest.mark.parametrize("order", [0, 1])

@@ -341,20 +341,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
 // the image border (the padding). This replaces the VALU transpose of the
 // general kernel's staging.
 //
-// A workgroup covers 32 output channels x one output row with 8 waves
-// (channel block lane, output-channel half), as the general kernel. (Two
-// rows per workgroup, with the weight fragments copied into LDS once for
-// both, halve the bytes per row but leave 96 of the 256 CUs idle at config
-// 5: 9.1 against 8.3 us.)
+// A workgroup covers CT = 32 or 64 output channels x one output row with
+// CT / 4 waves (channel block lane, 16-channel output group), as the general
+// kernel at CT = 32. (Two rows per workgroup, with the weight fragments
+// copied into LDS once for both, halve the bytes per row but leave 96 of the
+// 256 CUs idle at config 5: 9.1 against 8.3 us.)
 __host__ __device__ constexpr uint32_t conv3_stage_bytes(uint32_t c32, uint32_t nf) { return c32 * 96 * nf; }
+template <int CT>
 __host__ __device__ inline size_t conv3_main_lds_bytes(uint32_t c32, uint32_t nf)
 {
-    const size_t red = 4ull * cv::CO_TILE * 16 * nf * 4;
+    const size_t red = 4ull * CT * 16 * nf * 4;
     return conv3_stage_bytes(c32, nf) > red ? conv3_stage_bytes(c32, nf) : red;
 }
+template <int CT>
 __host__ __device__ inline size_t conv3_lds_bytes(uint32_t c32, uint32_t nf)
 {
-    return conv3_main_lds_bytes(c32, nf) + 2 * cv::CO_TILE * sizeof(float);
+    return conv3_main_lds_bytes<CT>(c32, nf) + 2 * CT * sizeof(float);
 }
 
 // The C32 channels x 3 rows x WI columns of image b around output row ho
@@ -362,11 +364,11 @@ __host__ __device__ inline size_t conv3_lds_bytes(uint32_t c32, uint32_t nf)
 // channel pos / CHB, row (pos % CHB) / ROWB, column bytes the rest. Rows
 // outside the image and channels past Ci read as zero (offset 2^31, or past
 // the resource's end; C32 planes stay under 2^31 bytes, so no offset wraps).
-template <int NF>
+template <int NF, int NW>
 __device__ __forceinline__ void conv3_stage(const ConvParams& p, __attribute__((address_space(3))) char* xs,
                                             uint32_t c32, uint32_t ho, uint32_t b, int wave, int lane)
 {
-    constexpr uint32_t ROWB = 32 * NF, CHB = 3 * ROWB, NW = 8;
+    constexpr uint32_t ROWB = 32 * NF, CHB = 3 * ROWB;
     const uint32_t plane_bytes = p.hi * ROWB;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const half_t*)p.x + (size_t)b * p.ci * p.hi * (16 * NF)), (short)0, (int)(p.ci * plane_bytes),
@@ -427,13 +429,13 @@ __device__ __forceinline__ void cv_finish8(float8v& v, const float8v& rr, bool r
     }
 }
 
-template <int NF>
+template <int NF, int CT>
 __device__ __forceinline__ void conv3_store(const ConvParams& p, const float* red, const float* epi_bs, uint32_t co0,
                                             uint32_t ho, uint32_t b)
 {
     constexpr uint32_t RW = NF * 16, Q8 = 2 * NF;
     const uint32_t it = threadIdx.x;
-    if (it >= cv::CO_TILE * Q8) return;
+    if (it >= CT * Q8) return;
     const uint32_t col = it / Q8, wo = (it % Q8) * 8, co = co0 + col;
     if (co >= p.co) return;
     const size_t o = ((size_t)b * p.co + co) * ((size_t)p.ho * RW) + (size_t)ho * RW + wo;
@@ -446,8 +448,8 @@ __device__ __forceinline__ void conv3_store(const ConvParams& p, const float* re
     const float* rp = red + (size_t)col * RW + wo;
     float8v v = *(const float8v*)rp;
 #pragma unroll
-    for (int w = 1; w < 4; ++w) v += *(const float8v*)(rp + (size_t)w * cv::CO_TILE * RW);
-    const float bias = p.bias ? epi_bs[col] : 0.f, sc = epi_bs[cv::CO_TILE + col];
+    for (int w = 1; w < 4; ++w) v += *(const float8v*)(rp + (size_t)w * CT * RW);
+    const float bias = p.bias ? epi_bs[col] : 0.f, sc = epi_bs[CT + col];
     const bool scaled = p.scale != nullptr;
     switch (p.epilogue) {
     case 1: cv_finish8<1>(v, rr, res, p.residual_order, sc, bias, scaled); break;
@@ -461,35 +463,36 @@ __device__ __forceinline__ void conv3_store(const ConvParams& p, const float* re
     else *(float8v*)((float*)p.out + o) = v;
 }
 
-template <int NF>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void conv3_tr_kernel(ConvParams p)
+template <int NF, int CT>
+__global__ __launch_bounds__(CT * 16) __attribute__((amdgpu_waves_per_eu(4))) void conv3_tr_kernel(ConvParams p)
 {
+    constexpr int NW = CT / 4;   // waves: 4 channel blocks x CT / 16 output-channel groups
     using namespace cv;
     constexpr uint32_t ROWB = 32 * NF, CHB = 3 * ROWB;
     extern __shared__ half8 smem[];
     __attribute__((address_space(3))) char* xs = (__attribute__((address_space(3))) char*)(
         __attribute__((address_space(3))) void*)smem;
     const uint32_t C32 = ci32(p.ci), nblk = C32 / 32;
-    float* epi_bs = (float*)((char*)smem + conv3_main_lds_bytes(C32, NF));   // [bias x 32, scale x 32]
+    float* epi_bs = (float*)((char*)smem + conv3_main_lds_bytes<CT>(C32, NF));   // [bias x 32, scale x 32]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cw = wave & 3, half = wave >> 2;   // channel-block lane, output-channel half
-    const uint32_t co0 = blockIdx.x * CO_TILE, ho = blockIdx.y, b = blockIdx.z;
+    const uint32_t co0 = blockIdx.x * CT, ho = blockIdx.y, b = blockIdx.z;
     const int fr = lane & 15, fg = lane >> 4;
 
     // the nine taps' A fragments of channel block cb (issued before the staging)
     half8 wa[9];
-    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * 2 + half, CO16 - 1);   // past Co: discarded
+    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * (CT / 16) + half, CO16 - 1);   // past Co: discarded
     auto load_w = [&](uint32_t cb) {
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap)
             wa[tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * nblk + cb) * 64 + lane) * 8);
     };
     if ((uint32_t)cw < nblk) load_w(cw);
-    conv3_stage<NF>(p, xs, C32, ho, b, wave, lane);
-    if (tid < 2 * CO_TILE) {   // bias and scale (a missing one reads the packed weight; ignored)
-        const half_t* src = tid < CO_TILE ? (p.bias ? (const half_t*)p.bias : p.wp)
-                                          : (p.scale ? (const half_t*)p.scale : p.wp);
-        epi_bs[tid] = (float)src[min(co0 + (tid % CO_TILE), p.co - 1)];
+    conv3_stage<NF, NW>(p, xs, C32, ho, b, wave, lane);
+    if (tid < 2 * CT) {   // bias and scale (a missing one reads the packed weight; ignored)
+        const half_t* src = tid < CT ? (p.bias ? (const half_t*)p.bias : p.wp)
+                                     : (p.scale ? (const half_t*)p.scale : p.wp);
+        epi_bs[tid] = (float)src[min(co0 + (tid % CT), p.co - 1)];
     }
     __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));   // vmcnt(0): copies landed
     __syncthreads();
@@ -533,9 +536,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[((size_t)cw * CO_TILE + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
+        for (int r = 0; r < 4; ++r) red[((size_t)cw * CT + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
     __syncthreads();
-    conv3_store<NF>(p, red, epi_bs, co0, ho, b);
+    conv3_store<NF, CT>(p, red, epi_bs, co0, ho, b);
 }
 
 // Whether the 3x3 LDS-transpose plan applies: fp16 NCHW rows of 16 NF
@@ -546,18 +549,32 @@ bool conv3_tr_ok(const ConvParams& p, int x_dt)
     return p.ks == 3 && p.stride == 1 && x_dt == DT_F16 && p.wi % 16 == 0 && nf >= 1 && nf <= 8 && p.wo == p.wi &&
            p.ho == p.hi && ((uintptr_t)p.x % 16) == 0 && ((uintptr_t)p.out % 32) == 0 &&
            ((uintptr_t)p.residual % 32) == 0 && (size_t)cv::ci32(p.ci) * p.hi * p.wi * 2 < (1ull << 31) &&
-           conv3_lds_bytes(cv::ci32(p.ci), nf) <= 160u * 1024u;
+           conv3_lds_bytes<64>(cv::ci32(p.ci), nf) <= 160u * 1024u;
 }
 
+template <int NF, int CT>
+static hipError_t launch_tr_ct(const ConvParams& p, hipStream_t s)
+{
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)conv3_tr_kernel<NF, CT>, 160 * 1024);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((conv3_tr_kernel<NF, CT>), dim3((p.co + CT - 1) / CT, p.ho, p.batch), dim3(CT * 16),
+                       conv3_lds_bytes<CT>(cv::ci32(p.ci), NF), s, p);
+    return hipGetLastError();
+}
+
+// 64 output channels per workgroup (16 waves) once 32-channel workgroups
+// would need more than one per CU: each input band is then staged once per
+// 64 channels, and no CU runs two workgroups back to back (config 5: 320
+// workgroups of 32 channels on 256 CUs, 8.1 us; 160 of 64, 7.3 us).
 template <int NF>
 static hipError_t launch_tr(const ConvParams& p, hipStream_t s)
 {
-    static PerDevice lds_once;
-    hipError_t e = set_max_lds(lds_once, (const void*)conv3_tr_kernel<NF>, 160 * 1024);
+    int cus = 0;
+    hipError_t e = device_cus(&cus);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(conv3_tr_kernel<NF>, dim3((p.co + cv::CO_TILE - 1) / cv::CO_TILE, p.ho, p.batch), dim3(512),
-                       conv3_lds_bytes(cv::ci32(p.ci), NF), s, p);
-    return hipGetLastError();
+    const uint64_t units32 = (uint64_t)((p.co + 31) / 32) * p.ho * p.batch;
+    return p.co > 32 && units32 > (uint64_t)cus ? launch_tr_ct<NF, 64>(p, s) : launch_tr_ct<NF, 32>(p, s);
 }
 
 size_t conv_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks)

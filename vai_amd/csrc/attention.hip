@@ -222,25 +222,6 @@ __device__ __forceinline__ void fa_issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buf
                                                  row0 * L::ROWB, 0, 0);
 }
 
-// The query tile's rows [0, 128) of q (rows past `rows` read as zero) into
-// stage 1: rows 0-63 where K goes, 64-127 where V goes, same swizzle.
-template <int D>
-__device__ __forceinline__ void fa_issue_q(const half_t* q, uint32_t rows, LDS_AS char* lds, const uint32_t* coff,
-                                           int wave)
-{
-    using L = fa::Lds<D>;
-    const __amdgpu_buffer_rsrc_t rq =
-        __builtin_amdgcn_make_buffer_rsrc((void*)q, (short)0, (int)((size_t)rows * D * 2), 0x00020000);
-    LDS_AS char* st = lds + L::STAGE + wave * L::COPIES * 1024;
-#pragma unroll
-    for (int j = 0; j < L::COPIES; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (LDS_AS void*)(st + j * 1024), 16, (int)coff[j], 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < L::COPIES; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (LDS_AS void*)(st + L::TILE + j * 1024), 16, (int)coff[j],
-                                                 fa::BKV * L::ROWB, 0, 0);
-}
-
 template <int N>
 __device__ __forceinline__ void fa_wait_vmcnt()
 {
@@ -353,27 +334,29 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         vofs[j] = lds0 + (vkey + vrow) * L::ROWB + ((4 * j + (vcol >> 3)) ^ swz_f((vkey + vrow) & 7)) * 16 +
                   (vcol & 7) * 2;
 
-    // Tile 0's copies into stage 0 and the query tile's 128 rows into stage 1
-    // (rows 0-63 where K goes, 64-127 where V goes, same swizzle; rows past
-    // Tq read as zero), all waited for in full. Then each wave reads its 32
-    // query rows as the B operand of S^T = K Q^T (lane l: query l % 32,
-    // head-dim values 16 s + 8 (l / 32) .. +7 of step s), and once every wave
-    // has (lgkmcnt(0), barrier) stage 1 is free for tile 1. From here on only
-    // LDS copies are counted by the waits below.
-    if (ntiles > 0) issue(0);
-    fa_issue_q<D>(Q + (size_t)q0 * D, Tq - q0, lds, coff, wave);
-    fa_wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
+    // The wave's 32 query rows go straight into VGPRs as the B operand of
+    // S^T = K Q^T (lane l: query l % 32, head-dim values 16 s + 8 (l / 32)
+    // .. +7 of step s; rows past Tq read as zero through the resource's
+    // range), issued first; then tile 0's copies and tile 1's, so that tile
+    // 1 is in flight during the prologue. Vector loads and the LDS copies
+    // each complete in issue order, so once at most the tile-1 copies are
+    // outstanding, the query rows and tile 0 have landed.
     half8 qf[KS];
     {
-        const int row = wave * QW + ql, rr = row % BKV;
-        LDS_AS const char* qs = lds + L::STAGE + (row / BKV) * L::TILE + rr * L::ROWB;
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(Q + (size_t)q0 * D), (short)0, (int)((size_t)(Tq - q0) * D * 2), 0x00020000);
+        const uint32_t qoff = (uint32_t)((wave * QW + ql) * D + 8 * hf) * 2;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) qf[s] = *(LDS_AS const half8*)(qs + swz<D>(rr, 2 * s + hf) * 16);
+        for (int s = 0; s < KS; ++s)
+            qf[s] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(qoff + 32 * s), 0, 0));
     }
-    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    if (ntiles > 1) issue(1);
+    if (ntiles > 0) issue(0);
+    if (ntiles > 1) {
+        issue(1);
+        fa_wait_vmcnt<2 * L::COPIES>();
+    } else {
+        fa_wait_vmcnt<0>();
+    }
     for (int t = 0; t < ntiles; ++t) {
         // tile t landed in every wave's share (tile t + 1's copies may be in flight)
         if (t > 0) {
@@ -704,7 +687,8 @@ bool attention_ok(const AttnParams& p)
 {
     return (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256) && p.hq > 0 && p.hkv > 0 &&
            p.hq % p.hkv == 0 && ((uintptr_t)p.q % 16) == 0 && ((uintptr_t)p.k % 16) == 0 &&
-           ((uintptr_t)p.v % 16) == 0 && (size_t)p.tkv * p.head_dim * 2 < (1ull << 31);
+           ((uintptr_t)p.v % 16) == 0 && (size_t)p.tkv * p.head_dim * 2 < (1ull << 31) &&
+           (size_t)p.tq * p.head_dim * 2 < (1ull << 31);
 }
 
 template <int D>

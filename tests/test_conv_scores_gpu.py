@@ -38,6 +38,10 @@ def run_conv(capi, x, w, b=None, s=None, r=None, out_dtype=np.float32, **kw):
     (32, 64, 3, 1, 20, 1, "SILU", np.float16),
     (24, 40, 3, 2, 17, 3, "SIGMOID", np.float16),
     (3, 16, 7, 2, 23, 1, "RELU", np.float16),
+    # 64-channel workgroups (more 32-channel ones than CUs) with output-channel tails:
+    (32, 96, 3, 2, 192, 1, "SILU", np.float16),    # 3x3 stride 2, vector epilogue
+    (64, 80, 1, 1, 100, 1, "RELU", np.float16),    # pointwise
+    (16, 48, 3, 2, 197, 2, "NONE", np.float16),    # odd output row: scalar epilogue, batch 2
 ])
 def test_conv(gpu, ci, co, ks, stride, hw, batch, epi, dt):
     rng = np.random.default_rng(0)

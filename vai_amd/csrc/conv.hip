@@ -13,14 +13,15 @@
 // conv weights once too, convolution.h:6224-6235).
 //
 // Forward kernel: one workgroup of 8 waves per (32 output channels, one
-// output row, image). It stages the k input rows it needs from NCHW into LDS
+// output row, image), or of 16 waves per 64 output channels when 32-channel
+// workgroups would outnumber the CUs (fp16 input). It stages the k input rows it needs from NCHW into LDS
 // transposed to [row][column][channel] (8 channels x 8 columns per work item:
 // eight 16-byte loads, a register transpose, eight 16-byte LDS writes), so 8
 // channels are one 16-byte LDS read; weight fragments come straight from the
 // packed buffer (L2-resident) into VGPRs, 1 KB of contiguous memory per
 // tap and wave (packing [tap][co][c] instead, a fragment load reads 16 rows x
 // 64 bytes and the loads cost 25% of the kernel time). Waves = 4 channel blocks x 2
-// halves of the 32 output channels; each runs v_mfma_f32_16x16x32_f16 over
+// (or 4) groups of 16 output channels; each runs v_mfma_f32_16x16x32_f16 over
 // every tap, their partial sums meet in LDS, and scale, bias, residual and
 // the activation are applied once per output with coalesced stores. A wave
 // stays within 128 VGPRs and only the input band occupies LDS, so two
@@ -44,11 +45,13 @@ inline __host__ __device__ uint32_t cip(uint32_t ci) { return ci32(ci) + 8; }   
 
 // LDS of the input band, later reused by the cross-wave sum (the larger of
 // the two); the epilogue's bias and scale follow it.
-__host__ __device__ inline size_t conv_main_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks)
+// (ct output channels per workgroup, nf 16-wide fragments of an output row)
+__host__ __device__ inline size_t conv_main_lds_bytes(uint32_t ci, uint32_t wi, uint32_t ks, uint32_t ct = cv::CO_TILE,
+                                                      uint32_t nf = cv::MAX_WO_FRAGS)
 {
     const size_t WiP = wi + 2 * (ks / 2), CIP = cv::cip(ci);
     const size_t stage = (size_t)ks * WiP * CIP * 2;
-    const size_t red = 4ull * cv::CO_TILE * 16 * cv::MAX_WO_FRAGS * 4;
+    const size_t red = 4ull * ct * 16 * nf * 4;
     return stage > red ? stage : red;
 }
 
@@ -82,16 +85,18 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(half_t* __restrict__ d
     }
 }
 
-// Scale, bias, residual and activation of a workgroup's 32 output channels x
-// one output row, from the partial sums of its four channel-block waves in
-// LDS (red[w][32][rw], positions along a row), with stores per output row.
-// 512 threads.
+// Scale, bias, residual and activation of a workgroup's CT output channels
+// x one output row, from the partial sums of its four channel-block waves in
+// LDS (red[w][CT][rw], positions along a row), with stores per output row.
+// CT * 16 threads (NW = CT / 4 waves).
+template <int CT>
 __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red, uint32_t rw, const float* epi_bs,
                                            uint32_t co0, uint32_t ho, uint32_t b)
 {
     using namespace cv;
+    constexpr int NW = CT / 4, NT = NW * 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int EPI_COLS = CO_TILE / 8;   // output channels per wave in the scalar path
+    constexpr int EPI_COLS = CT / NW;   // output channels per wave in the scalar path
     const size_t HoWo = (size_t)p.ho * p.wo;
     const bool vec4 = p.wo % 4 == 0 && (uintptr_t)p.out % 16 == 0 && (uintptr_t)p.residual % 16 == 0;
     if (vec4) {
@@ -99,14 +104,14 @@ __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red
         // 16-byte partial-sum reads, one 16-byte (fp32) or 8-byte (fp16)
         // store. A row of Wo outputs stays 16-byte aligned (Ho Wo and Wo
         // are multiples of 4).
-        const uint32_t q4 = p.wo / 4, items = CO_TILE * q4;
-        for (uint32_t it = tid; it < items; it += 512) {
+        const uint32_t q4 = p.wo / 4, items = CT * q4;
+        for (uint32_t it = tid; it < items; it += NT) {
             const uint32_t col = it / q4, wo = (it % q4) * 4, co = co0 + col;
             if (co >= p.co) continue;
             float4v v = *(const float4v*)(red + (size_t)col * rw + wo);
 #pragma unroll
-            for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CO_TILE + col) * rw + wo);
-            const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
+            for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CT + col) * rw + wo);
+            const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CT + col] : 1.f;
             const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
             float4v rr = (float4v)0.f;
             if (p.residual) {
@@ -126,7 +131,7 @@ __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red
         }
         return;
     }
-    // Outputs (co0 + wave + 8 i, wo = lane + 64 k); residuals first, all
+    // Outputs (co0 + wave + NW i, wo = lane + 64 k); residuals first, all
     // loads in flight together (indices clamped, unused values discarded).
     constexpr int EPI_W = MAX_WO_FRAGS * 16 / 64;
     float rv[EPI_COLS][EPI_W] = {};
@@ -136,7 +141,7 @@ __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red
         for (int i = 0; i < EPI_COLS; ++i)
 #pragma unroll
             for (int k = 0; k < EPI_W; ++k) {
-                const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
+                const uint32_t co = min(co0 + wave + NW * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
                 const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
                 rv[i][k] = r16 ? (float)((const half_t*)p.residual)[o] : 0.f;
             }
@@ -145,23 +150,23 @@ __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red
             for (int i = 0; i < EPI_COLS; ++i)
 #pragma unroll
                 for (int k = 0; k < EPI_W; ++k) {
-                    const uint32_t co = min(co0 + wave + 8 * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
+                    const uint32_t co = min(co0 + wave + NW * i, p.co - 1), wo = min(lane + 64 * k, p.wo - 1);
                     rv[i][k] = ((const float*)p.residual)[((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo];
                 }
         }
     }
 #pragma unroll
     for (int i = 0; i < EPI_COLS; ++i) {
-        const uint32_t col = wave + 8 * i, co = co0 + col;
+        const uint32_t col = wave + NW * i, co = co0 + col;
         if (co >= p.co) break;
-        const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CO_TILE + col] : 1.f;
+        const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CT + col] : 1.f;
         const size_t obase = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo;
 #pragma unroll
         for (int k = 0; k < EPI_W; ++k) {
             const uint32_t wo = lane + 64 * k;
             if (wo >= p.wo) break;
-            float v = red[(size_t)col * rw + wo] + red[((size_t)CO_TILE + col) * rw + wo] +
-                      red[((size_t)2 * CO_TILE + col) * rw + wo] + red[((size_t)3 * CO_TILE + col) * rw + wo];
+            float v = red[(size_t)col * rw + wo] + red[((size_t)CT + col) * rw + wo] +
+                      red[((size_t)2 * CT + col) * rw + wo] + red[((size_t)3 * CT + col) * rw + wo];
             v = p.scale ? fmaf(v, sc, bias) : v + bias;
             const float rr = rv[i][k];
             if (p.residual && p.residual_order == 1) v += rr;
@@ -172,26 +177,27 @@ __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red
     }
 }
 
-template <int KS, int NF, typename TI>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void conv_kernel(ConvParams p)
+template <int KS, int NF, typename TI, int CT>
+__global__ __launch_bounds__(CT * 16) __attribute__((amdgpu_waves_per_eu(4))) void conv_kernel(ConvParams p)
 {
     using namespace cv;
+    constexpr int NT = CT * 16;   // threads: 4 channel blocks x CT / 16 output-channel groups, one wave each
     extern __shared__ half8 smem[];
     const uint32_t C32 = ci32(p.ci), CIP = cip(p.ci);
     constexpr int PAD = KS / 2;
     const uint32_t WiP = p.wi + 2 * PAD;
     half_t* xs = (half_t*)smem;                              // [KS][WiP][CIP]
-    float* epi_bs = (float*)((char*)smem + conv_main_lds_bytes(p.ci, p.wi, KS));   // [bias x 32, scale x 32]
+    float* epi_bs = (float*)((char*)smem + conv_main_lds_bytes(p.ci, p.wi, KS, CT, NF));   // [bias x CT, scale x CT]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cw = wave & 3, half = wave >> 2;               // channel-block lane, output-channel half
-    const uint32_t co0 = blockIdx.x * CO_TILE, ho = blockIdx.y, b = blockIdx.z;
+    const uint32_t co0 = blockIdx.x * CT, ho = blockIdx.y, b = blockIdx.z;
     const int fr = lane & 15, fg = lane >> 4;
     const uint32_t nblk = C32 / 32;
 
     // A fragments straight from the packed weight (L2-resident, shared by all
     // blocks): issued first so their latency hides behind the input staging.
     half8 wa[KS * KS];
-    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * 2 + half, CO16 - 1);   // past Co: discarded
+    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * (CT / 16) + half, CO16 - 1);   // past Co: discarded
     auto load_w = [&](uint32_t cb) {
 #pragma unroll
         for (int tap = 0; tap < KS * KS; ++tap)
@@ -217,7 +223,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
         const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
             (void*)((const TI*)p.x + (size_t)b * p.ci * plane), (short)0,
             (int)std::min<size_t>((size_t)p.ci * plane * sizeof(TI), 0x7FFFFFFF), 0x00020000);
-        for (uint32_t it = tid; it < items; it += 512) {
+        for (uint32_t it = tid; it < items; it += NT) {
             const uint32_t cg = it % ngc, rest = it / ngc, wg = rest % ngw, r = rest / ngw;
             const int hi = (int)(ho * p.stride) + (int)r - PAD;
             const bool row_ok = hi >= 0 && hi < (int)p.hi;
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
                 if (w0 + j < p.wi) *(half8*)(dst + (size_t)j * CIP) = col[j];
         }
         // the zero padding columns
-        for (uint32_t i = tid; i < (uint32_t)(KS * 2 * PAD) * (C32 / 8); i += 512) {
+        for (uint32_t i = tid; i < (uint32_t)(KS * 2 * PAD) * (C32 / 8); i += NT) {
             const uint32_t cg = i % (C32 / 8), rc = i / (C32 / 8), r = rc / (2 * PAD), e = rc % (2 * PAD);
             const uint32_t w = e < PAD ? e : PAD + p.wi + (e - PAD);
             *(half8*)(xs + ((size_t)r * WiP + w) * CIP + cg * 8) = (half8)(half_t)0;
@@ -276,10 +282,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
         // bias and scale of the tile's output channels, for the epilogue
         // (unconditional loads: a missing one reads the packed weight, at
         // least Co values long, and the epilogue ignores it)
-        if (tid < 2 * CO_TILE) {
-            const half_t* src = tid < CO_TILE ? (p.bias ? (const half_t*)p.bias : p.wp)
-                                              : (p.scale ? (const half_t*)p.scale : p.wp);
-            epi_bs[tid] = (float)src[min(co0 + (tid % CO_TILE), p.co - 1)];
+        if (tid < 2 * CT) {
+            const half_t* src = tid < CT ? (p.bias ? (const half_t*)p.bias : p.wp)
+                                         : (p.scale ? (const half_t*)p.scale : p.wp);
+            epi_bs[tid] = (float)src[min(co0 + (tid % CT), p.co - 1)];
         }
     }
     __syncthreads();
@@ -314,16 +320,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void c
 
     // ---- cross-wave sum in LDS, then the epilogue ----
     // D[i][j] of a 16x16 fragment sits in lane j + 16*(i/4), register i%4.
-    float* red = (float*)smem;                               // [4 channel lanes][32 co][16*nf positions]
+    float* red = (float*)smem;                               // [4 channel lanes][CT co][16*nf positions]
     const uint32_t rw = (uint32_t)nf * 16;
 #pragma unroll
     for (int f = 0; f < MAX_WO_FRAGS; ++f)
         if (f < nf)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                red[((size_t)cw * CO_TILE + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
+                red[((size_t)cw * CT + half * 16 + fg * 4 + r) * rw + f * 16 + fr] = acc[f][r];
     __syncthreads();
-    conv_store(p, red, rw, epi_bs, co0, ho, b);
+    conv_store<CT>(p, red, rw, epi_bs, co0, ho, b);
 }
 
 // ---- 3x3, stride 1, fp16 NCHW input, row width 16 NF (config 5's shape) ----
@@ -600,13 +606,29 @@ hipError_t conv_pack_weight(half_t* dst, const half_t* w, uint32_t ci, uint32_t 
     return hipGetLastError();
 }
 
+// fp16 input takes 64 output channels per workgroup (16 waves) once 32-channel
+// workgroups would outnumber the CUs and the 64-channel sums fit LDS: no CU
+// then runs two workgroups back to back, and each input band is staged once
+// per 64 channels (as the 3x3 stride-1 kernel below does).
 template <int KS, int NF>
 static hipError_t launch_nf(const ConvParams& p, int x_dt, size_t lds, hipStream_t s)
 {
-    auto kern = x_dt == DT_F16 ? conv_kernel<KS, NF, half_t> : conv_kernel<KS, NF, float>;
-    static PerDevice lds_once[2];
-    hipError_t e = set_max_lds(lds_once[x_dt == DT_F16], (const void*)kern, 160 * 1024);
+    int cus = 0;
+    hipError_t e = device_cus(&cus);
     if (e != hipSuccess) return e;
+    const uint64_t units32 = (uint64_t)((p.co + 31) / 32) * p.ho * p.batch;
+    const size_t lds64 = conv_main_lds_bytes(p.ci, p.wi, KS, 64, NF) + 2 * 64 * sizeof(float);
+    if (x_dt == DT_F16 && p.co > 32 && units32 > (uint64_t)cus && lds64 <= 160u * 1024u) {
+        static PerDevice lds_once64;
+        if ((e = set_max_lds(lds_once64, (const void*)conv_kernel<KS, NF, half_t, 64>, 160 * 1024)) != hipSuccess)
+            return e;
+        hipLaunchKernelGGL((conv_kernel<KS, NF, half_t, 64>), dim3((p.co + 63) / 64, p.ho, p.batch), dim3(1024), lds64,
+                           s, p);
+        return hipGetLastError();
+    }
+    auto kern = x_dt == DT_F16 ? conv_kernel<KS, NF, half_t, 32> : conv_kernel<KS, NF, float, 32>;
+    static PerDevice lds_once[2];
+    if ((e = set_max_lds(lds_once[x_dt == DT_F16], (const void*)kern, 160 * 1024)) != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3((p.co + cv::CO_TILE - 1) / cv::CO_TILE, p.ho, p.batch), dim3(512), lds, s, p);
     return hipGetLastError();
 }

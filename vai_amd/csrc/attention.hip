@@ -448,10 +448,14 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
             const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -__builtin_inff() ? 0.f : mnew));
             l *= alpha;
             m = mnew;
+            // before the unit's first P.V, O is zero in every row: nothing to
+            // rescale (every unit's first tile moves m from -inf)
+            if (t > 0) {
 #pragma unroll
-            for (int d = 0; d < DF; ++d)
+                for (int d = 0; d < DF; ++d)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[d][r] = fa_scale_acc(o[d][r], alpha);
+                    for (int r = 0; r < 16; ++r) o[d][r] = fa_scale_acc(o[d][r], alpha);
+            }
         }
         const float mref = m == -__builtin_inff() ? 0.f : m;
         half8 pb[4];   // P^T operand of key step kk: registers 8 (kk % 2) .. +7 of block kk / 2

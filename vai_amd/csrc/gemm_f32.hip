@@ -23,6 +23,8 @@
 // the k order is 4*(l/16) + q on both operands and every product is still
 // summed once. Rows past M or N read as zero through the buffer resource's
 // range check.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 #include "launch_once.h"
@@ -154,44 +156,51 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
                                                      (int)(coff + u * row8), kb, 0, 0);
     };
     // Fragment reads: lane l takes row (16*f + l%16), logical chunk h*4 + l/16.
+    // Half h of a stage (16 of its 32 k) goes into register set h; the
+    // next stage's first half is read while this stage's second half runs
+    // its MFMAs, so no stage starts on an LDS read latency.
     const uint32_t fr = lane & 15, fc = lane >> 4;
-    auto compute = [&](int slot) __attribute__((always_inline)) {
+    float4v fa[2][2], fb[2][NF];
+    auto read = [&](int slot, auto H) __attribute__((always_inline)) {
+        constexpr int h = decltype(H)::value;
         LDS_AS const char* src = ring + slot * STAGE;
+        const uint32_t off = (fr * 8 + ((h * 4 + fc) ^ (fr % 8))) * 16;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t off = (fr * 8 + ((h * 4 + fc) ^ (fr % 8))) * 16;
-            float4v a[2], b[NF];
+        for (int i = 0; i < 2; ++i) fa[h][i] = *(LDS_AS const float4v*)(src + off + i * 16 * 128);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = *(LDS_AS const float4v*)(src + off + i * 16 * 128);
+        for (int j = 0; j < NF; ++j) fb[h][j] = *(LDS_AS const float4v*)(src + 32 * 128 + off + j * 16 * 128);
+    };
+    auto mma = [&](auto H) __attribute__((always_inline)) {
+        constexpr int h = decltype(H)::value;
 #pragma unroll
-            for (int j = 0; j < NF; ++j) b[j] = *(LDS_AS const float4v*)(src + 32 * 128 + off + j * 16 * 128);
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < NF; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
-        }
+                for (int j = 0; j < NF; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[h][i][q], fb[h][j][q], acc[i][j], 0, 0, 0);
     };
     if (n > 0) {
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) issue(s, c_lo + s);
-        int c = 0;
-        for (; c + SLOTS <= n; c += SLOTS) {
-            static_for<SLOTS>([&](auto S) __attribute__((always_inline)) {
-                f32k_wait_vmcnt<(SLOTS - 1) * LOADS>();   // this stage's copies have landed
-                compute(S);
-                f32k_wait_lgkmcnt0();                      // its reads are done: the slot is free
-                issue(S, c_lo + c + S + SLOTS);
-            });
-        }
-        static_for<SLOTS - 1>([&](auto S) __attribute__((always_inline)) {
-            if (c + S < n) {
-                f32k_wait_vmcnt<0>();
-                compute(S);
+        f32k_wait_vmcnt<(SLOTS - 1) * LOADS>();   // stage 0 has landed
+        read(0, std::integral_constant<int, 0>{});
+        int slot = 0;
+        for (int c = 0; c < n; ++c) {
+            const int next = slot + 1 == SLOTS ? 0 : slot + 1;
+            read(slot, std::integral_constant<int, 1>{});
+            mma(std::integral_constant<int, 0>{});
+            if (c + 1 < n) {
+                // stage c + 1 has landed: stages up to c + 2 were issued, and
+                // only c + 2's copies may still be in flight
+                f32k_wait_vmcnt<(SLOTS - 2) * LOADS>();
+                read(next, std::integral_constant<int, 0>{});
             }
-        });
+            mma(std::integral_constant<int, 1>{});
+            f32k_wait_lgkmcnt0();                      // every read of this slot has returned
+            issue(slot, c_lo + c + SLOTS);
+            slot = next;
+        }
     }
     f32k_wait_vmcnt<0>();   // the clamped copies land before the ring is reused
     __syncthreads();

@@ -7,7 +7,10 @@
 //  * one workgroup per 128x128 tile (64x64 when a mask applies) of one head,
 //    each head's tiles on one XCD when the heads come in multiples of 8;
 //    tiles the mask hides entirely are written as -inf and never touch Q, K
-//    or the matrix cores;
+//    or the matrix cores; under a plain causal mask over a square S (a
+//    multiple of 64) only the tiles on and below the diagonal are launched,
+//    and each writes its mirror tile's -inf while its Q/K stages load
+//    (config 4: 10.7-11.0 against 11.4-11.6 us with every tile launched);
 //  * Q and K rows are copied global->LDS (buffer_load ... lds) in 64-wide
 //    head-dim stages, double buffered; 4 waves x (T/2 x T/2 of 32x32x16
 //    MFMAs); 64 KB (32 KB) of LDS, so two (four) workgroups share a CU and
@@ -51,8 +54,12 @@ __device__ __forceinline__ void sc_wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int T>
-__global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParams p)
+// TRI (square causal scores, Tq == Tkv a multiple of T, no window or block
+// list): the grid holds only the n (n + 1) / 2 tiles on and below the
+// diagonal, and each tile below it first stores the -inf of its mirror tile
+// above the diagonal, while its own Q/K stages are on their way.
+template <int T, bool TRI = false>
+__global__ __launch_bounds__(256, T == 128 ? 2 : (TRI ? 5 : 4)) void scores_kernel(GemmParams p)
 {
     using namespace sc;
     constexpr int WF = Tile<T>::WF, STAGE = Tile<T>::STAGE, LOADS = Tile<T>::LOADS, HT = T / 2;
@@ -72,12 +79,35 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : 4) void scores_kernel(GemmParam
         tx = tile % gridDim.x;
         ty = tile / gridDim.x;
     }
+    if constexpr (TRI) {
+        // lower-triangle tile k (row by row): row a holds a + 1 tiles
+        const uint32_t k = ty * gridDim.x + tx;
+        uint32_t a = (uint32_t)((__builtin_sqrtf(8.0f * (float)k + 1.0f) - 1.0f) * 0.5f);
+        while (a * (a + 1) / 2 > k) --a;
+        while ((a + 1) * (a + 2) / 2 <= k) ++a;
+        ty = a;
+        tx = k - a * (a + 1) / 2;
+    }
     const uint32_t m0 = ty * T, n0 = tx * T;
     const uint32_t M = p.M, N = p.N, K = p.K;
     float* S = (float*)p.C + bz * p.c_batch_stride;
 
+    if constexpr (TRI) {
+        if (ty > tx) {
+            // the mirror tile (tx, ty): rows above the diagonal block, all
+            // hidden; issued before the Q/K copies, so that the waits below,
+            // which count younger operations only, never pass on a store
+            constexpr int LPR = HT / 4, RPI = 64 / LPR;
+            const float4v ninf = (float4v)(-__builtin_inff());
+            const uint32_t r0 = tx * T + wm * HT, c = ty * T + wn * HT + (lane % LPR) * 4;
+#pragma unroll
+            for (int it = 0; it < HT / RPI; ++it)
+                __builtin_nontemporal_store(ninf, (float4v*)(S + (size_t)(r0 + it * RPI + lane / LPR) * N + c));
+        }
+    }
+
     // Tiles the mask hides entirely: -inf, 16 bytes per lane.
-    {
+    if constexpr (!TRI) {
         // the tile's rows read at most keys [key_start(first row), key_end(last row))
         const uint32_t last = (m0 + T < M ? m0 + T : M) - 1;
         const bool hidden = (int64_t)n0 >= p.mask.key_end(last) || (int64_t)n0 + T <= p.mask.key_start(m0);
@@ -247,12 +277,26 @@ static hipError_t scores_launch_t(const GemmParams& p, hipStream_t s)
     return hipGetLastError();
 }
 
+static hipError_t scores_launch_tri(const GemmParams& p, hipStream_t s)
+{
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)scores_kernel<64, true>, sc::Tile<64>::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    const uint32_t n = p.M / 64;
+    hipLaunchKernelGGL((scores_kernel<64, true>), dim3(n * (n + 1) / 2, 1, p.batch), dim3(256), sc::Tile<64>::LDS_BYTES,
+                       s, p);
+    return hipGetLastError();
+}
+
 // Masked scores use 64x64 tiles: hidden tiles are then finer, and four
 // times as many workgroups spread the unevenly sized tiles over the CUs
 // (config 4 on MI355X: 12.8 us against 14.1 us with 128x128 tiles); unmasked
 // scores keep 128x128 tiles (fewer Q/K re-reads, 12.8 against 13.2 us).
 hipError_t scores_launch(const GemmParams& p, hipStream_t s)
 {
+    if (p.causal && p.mask.blocks == 1 && p.mask.bits == 1 && p.span == 0 && p.mask.span == 0 && p.M == p.N &&
+        p.causal_offset == 0 && p.M % 64 == 0)
+        return scores_launch_tri(p, s);
     return (p.causal || p.span || p.mask.blocks > 1) ? scores_launch_t<64>(p, s) : scores_launch_t<128>(p, s);
 }
 

@@ -4,11 +4,14 @@
 // runs with fp32 staging (stageF32) in the reference.
 //
 // fp32 matrix cores deliver 1/16 of the fp16 rate, so a small fp32 GEMM is
-// bound by how many SIMDs stay busy, not by bytes. One workgroup (4 waves)
-// owns a 32 x 16*NF output tile and the full K: the waves split K four ways
-// and their partial tiles are summed once through LDS, so no split-K
-// partials go to memory and there is no second launch. NF is chosen at plan
-// time so that the tile count lands on (a multiple of) the CU count.
+// bound by how many SIMDs stay busy, not by bytes. One workgroup (8 waves,
+// two per SIMD, so that one wave's MFMAs cover the other's waits) owns a
+// 32 x 16*NF output tile and the full K: the waves split K eight ways and
+// their partial tiles are summed once through LDS, so no split-K partials go
+// to memory and there is no second launch. NF (at most 3: the eight rings
+// fill the 160 KB of LDS) is chosen at plan time so that the tile count lands
+// on (a multiple of) the CU count. (Four waves with three-stage rings: 8.87
+// against 8.68-8.71 us on config 1, both builds in one run.)
 //
 // Operand staging: each wave streams its own K range through a private ring
 // of LDS stages (no workgroup barrier in the loop). A stage is 32 k of the
@@ -32,8 +35,8 @@
 namespace vai_dev {
 
 namespace f32k {
-constexpr int WAVES = 4;
-constexpr int SLOTS = 3;   // LDS stages per wave (two copies ahead)
+constexpr int WAVES = 8;   // two per SIMD: one's MFMAs cover the other's waits
+constexpr int SLOTS = 2;   // LDS stages per wave (one copy ahead)
 constexpr int KC = 32;     // k per stage: 128 bytes of each row
 }
 
@@ -54,34 +57,29 @@ constexpr size_t f32k_stage_bytes() { return (size_t)(32 + 16 * NF) * 128; }
 template <int NF>
 constexpr size_t f32k_lds_bytes()
 {
-    const size_t ring = 4 * f32k::SLOTS * f32k_stage_bytes<NF>();
-    const size_t red = (size_t)4 * 2 * NF * 4 * 64 * 4;
+    const size_t ring = (size_t)f32k::WAVES * f32k::SLOTS * f32k_stage_bytes<NF>();
+    const size_t red = (size_t)f32k::WAVES * 2 * NF * 4 * 64 * 4;
     return ring > red ? ring : red;
 }
 
 // fp32 output, no residual, bias absent or one [N] row: the activation is
 // compile-time (EPI 6: the runtime epilogue code).
 template <int NF, uint32_t EPI>
-__device__ __forceinline__ void f32k_store(const GemmParams& p, const float (&v)[2][NF], const float (&cbias)[NF],
+__device__ __forceinline__ void f32k_store(const GemmParams& p, const float (&v)[NF], const float (&cbias)[NF],
                                            uint32_t row, uint32_t col)
 {
     const uint32_t M = p.M, N = p.N;
     const float s = p.scalar_scale;
+    if (row >= M) return;
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
         const uint32_t c = col + j * 16;
-        if (c >= N) continue;
-        const float cb = cbias[j];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t r = row + i * 16;
-            if (r < M) ((float*)p.C)[(size_t)r * N + c] = s * epilogue(v[i][j] + cb, EPI == 6 ? p.epilogue : EPI);
-        }
+        if (c < N) ((float*)p.C)[(size_t)row * N + c] = s * epilogue(v[j] + cbias[j], EPI == 6 ? p.epilogue : EPI);
     }
 }
 
 template <int NF>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
+__global__ __launch_bounds__(64 * f32k::WAVES) void gemm_f32_kernel(GemmParams p)
 {
     using namespace f32k;
     constexpr int BM = 32, BN = 16 * NF;
@@ -206,9 +204,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
     __syncthreads();
     float (*red)[2 * NF * 4][64] = (float (*)[2 * NF * 4][64])lds_raw;
 
-    // The four partial tiles meet in LDS; every thread then finishes 2*NF
-    // outputs. Thread (wave w, lane l) takes register r = w of every fragment
-    // (i, j): row i*16 + 4*(l/16) + w, column j*16 + l%16.
+    // The WAVES partial tiles meet in LDS; every thread then finishes NF
+    // outputs. Thread (wave w, lane l) takes register r = w % 4 of the
+    // fragments (w / 4, j): row 16 (w / 4) + 4 (l / 16) + r, column 16 j + l % 16.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -216,17 +214,17 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][(i * NF + j) * 4 + r][lane] = acc[i][j][r];
     __syncthreads();
-    const uint32_t col_l = lane & 15, row_l = (lane >> 4) * 4 + wave;
-    float v[2][NF];
+    static_assert(WAVES == 8, "two fragment rows x four registers");
+    const int fi = wave >> 2, fr4 = wave & 3;
+    const uint32_t col_l = lane & 15, row_l = fi * 16 + (lane >> 4) * 4 + fr4;
+    float v[NF];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < NF; ++j) {
+        float a = 0.f;
 #pragma unroll
-        for (int j = 0; j < NF; ++j) {
-            float a = 0.f;
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) a += red[w][(i * NF + j) * 4 + wave][lane];
-            v[i][j] = a;
-        }
+        for (int w = 0; w < WAVES; ++w) a += red[w][(fi * NF + j) * 4 + fr4][lane];
+        v[j] = a;
+    }
     const bool plain = p.c_dtype == 0 && !p.residual && (!p.bias || p.bias_repeat == N);
     if (plain) {
         switch (p.epilogue) {
@@ -237,19 +235,16 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p)
         }
         return;
     }
+    const uint32_t row = r0 + row_l;
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
         const uint32_t col = c0 + j * 16 + col_l;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t row = r0 + i * 16 + row_l;
-            if (row < M && col < N) {
-                const size_t o = (size_t)row * N + col;
-                const float bb = p.bias ? ld(p.bias, p.bias_dtype, p.bias_repeat ? o % p.bias_repeat : o) : 0.f;
-                const float res = p.residual
-                    ? ld(p.residual, p.residual_dtype, p.residual_repeat ? o % p.residual_repeat : o) : 0.f;
-                st(p.C, p.c_dtype, o, finish(v[i][j] + bb, res, p.epilogue, p.residual_order, p.scalar_scale));
-            }
+        if (row < M && col < N) {
+            const size_t o = (size_t)row * N + col;
+            const float bb = p.bias ? ld(p.bias, p.bias_dtype, p.bias_repeat ? o % p.bias_repeat : o) : 0.f;
+            const float res = p.residual
+                ? ld(p.residual, p.residual_dtype, p.residual_repeat ? o % p.residual_repeat : o) : 0.f;
+            st(p.C, p.c_dtype, o, finish(v[j] + bb, res, p.epilogue, p.residual_order, p.scalar_scale));
         }
     }
 }
@@ -268,7 +263,7 @@ int gemm_f32_nf(uint32_t M, uint32_t N, uint32_t cus)
 {
     int best = 1;
     uint64_t best_cost = ~0ull;
-    for (int nf = 4; nf >= 1; --nf) {
+    for (int nf = 3; nf >= 1; --nf) {   // NF = 4 would need 192 KB of LDS rings
         const uint64_t tiles = (uint64_t)((M + 31) / 32) * ((N + 16 * nf - 1) / (16 * nf));
         const uint64_t cost = (tiles + cus - 1) / cus * nf;
         if (cost < best_cost) { best_cost = cost; best = nf; }
@@ -284,7 +279,7 @@ static hipError_t f32k_launch(const GemmParams& p, hipStream_t s)
     hipError_t e = set_max_lds(lds_once, (const void*)gemm_f32_kernel<NF>, (int)f32k_lds_bytes<NF>());
     if (e != hipSuccess) return e;
     const uint32_t tiles = ((p.M + 31) / 32) * ((p.N + 16 * NF - 1) / (16 * NF));
-    hipLaunchKernelGGL(gemm_f32_kernel<NF>, dim3(tiles), dim3(256), f32k_lds_bytes<NF>(), s, p);
+    hipLaunchKernelGGL(gemm_f32_kernel<NF>, dim3(tiles), dim3(64 * f32k::WAVES), f32k_lds_bytes<NF>(), s, p);
     return hipGetLastError();
 }
 
@@ -294,7 +289,6 @@ hipError_t gemm_f32_launch(const GemmParams& p, int nf, hipStream_t s)
     case 1: return f32k_launch<1>(p, s);
     case 2: return f32k_launch<2>(p, s);
     case 3: return f32k_launch<3>(p, s);
-    case 4: return f32k_launch<4>(p, s);
     default: return hipErrorInvalidValue;
     }
 }

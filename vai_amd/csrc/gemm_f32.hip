@@ -189,8 +189,8 @@ __global__ __launch_bounds__(64 * f32k::WAVES) void gemm_f32_kernel(GemmParams p
             read(slot, std::integral_constant<int, 1>{});
             mma(std::integral_constant<int, 0>{});
             if (c + 1 < n) {
-                // stage c + 1 has landed: stages up to c + 2 were issued, and
-                // only c + 2's copies may still be in flight
+                // stage c + 1 has landed: stages up to c + SLOTS - 1 were
+                // issued, and only the SLOTS - 2 after c + 1 may be in flight
                 f32k_wait_vmcnt<(SLOTS - 2) * LOADS>();
                 read(next, std::integral_constant<int, 0>{});
             }

@@ -218,16 +218,27 @@ typedef struct {
 vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t stream);
 
 /* ---------------------------------------------------------------------------
- * Attention: O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h/g,j,:] + mask)
- * V[b,h/g,j,:], g = Hq/Hkv, with the mask rule of vai_attn_scores_launch
- * (causal, span, or a block mask). fp32 softmax statistics and accumulation; P is rounded to
- * fp16 for the P.V product. Q [batch,Hq,Tq,D], K/V [batch,Hkv,Tkv,D] fp16,
- * D in {64, 128, 256}; O [batch,Hq,Tq,D] in o_dtype (f32 or f16). A query
- * with no visible key gives zeros. Long key ranges may be split over
- * workgroups and merged (then a workspace is needed). Replaces the
- * flash-attention dispatch of
- * the reference's Attention node (/root/reference/vai/nodes/attention.h:
- * 979-1304, shaders/attention-fa.comp) for the no-cache case.
+ * Attention: O[b,i,h,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h/g,j,:] +
+ * mask) V[b,h/g,j,:], g = Hq/Hkv -- the reference's Attention node without a
+ * KV cache (/root/reference/vai/nodes/attention.h:77-79, 979-1304;
+ * shaders/attention-fa.comp, attention.comp, attention-fa-reduce.comp).
+ *   Q [batch,Hq,Tq,D] in q_dtype, K / V [batch,Hkv,Tkv,D] in kv_dtype (f32 or
+ *   f16 each, as typeI / typeKV, attention.h:86-88); O token-major
+ *   [batch,Tq,Hq,D] in o_dtype (attention-fa.comp:8,96 and attention.h:
+ *   1220-1223), so that [batch,Tq,Hq*D] is a reshape.
+ *   Queries and keys align at their ends (query i sits at key i + Tkv - Tq).
+ *   The mask is vai_attn_scores_launch's: causal = 0 and mask_blocks = 0 is
+ *   no mask at all, the reference's default when setCausalMask was never
+ *   called (attention.h:129). A query with no visible key gives zeros.
+ *   Any head dim 1..2048. D % 8 == 0 with 16 <= D <= 256 (the reference's
+ *   flash-attention gate, attention.h:916-945) and 16-byte aligned operands
+ *   take the MFMA flash kernel: fp32 softmax statistics and accumulation,
+ *   Q.K^T and P.V on fp16 operands (fp32 Q is rounded to fp16 as the
+ *   reference's f16-staged tiles do, fp32 K / V are rounded into workspace
+ *   copies first, P enters P.V as fp16). Every other head dim takes a plain
+ *   fp32 kernel (the reference's naive attention.comp role).
+ *   Long key ranges may be split over workgroups and merged; fp32 K / V and
+ *   the split need vai_attention_workspace_size() bytes of workspace.
  * ------------------------------------------------------------------------- */
 typedef struct {
     void* out;
@@ -235,7 +246,8 @@ typedef struct {
     const void* k;
     const void* v;
     int32_t o_dtype;
-    int32_t i_dtype;              /* VAI_DTYPE_F16 */
+    int32_t q_dtype;              /* VAI_DTYPE_F32 or VAI_DTYPE_F16 */
+    int32_t kv_dtype;             /* VAI_DTYPE_F32 or VAI_DTYPE_F16, K and V alike */
     uint32_t batch, hq, hkv, tq, tkv, head_dim;
     float scale;                  /* 0: 1/sqrt(head_dim), as attention.h:1254 */
     uint32_t causal;
@@ -248,9 +260,10 @@ typedef struct {
 } vai_attention_args;
 
 vai_status vai_attention_launch(const vai_attention_args* args, vai_stream_t stream);
-/* Bytes of workspace a launch needs: nonzero when the query tiles alone do
- * not fill the GPU and long key ranges are split over workgroups (partial
- * results merged by a second pass, the split-K of attention-fa-reduce.comp). */
+/* Bytes of workspace a launch needs: nonzero when fp32 K / V take the flash
+ * kernel (their fp16 copies), or when the query tiles alone do not fill the
+ * GPU and long key ranges are split over workgroups (partial results merged by
+ * a second pass, the split-K of attention-fa-reduce.comp). */
 size_t vai_attention_workspace_size(const vai_attention_args* args);
 
 /* ---------------------------------------------------------------------------

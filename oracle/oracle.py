@@ -203,12 +203,21 @@ def attn_scores(q, k, *, scale=None, causal=True, span=0, blocks=None):
     return out
 
 
-def attention(q, k, v, *, scale=None, causal=True, span=0, out_dtype=np.float32, blocks=None):
-    """O = softmax(S) V per query row, S = attn_scores(q, k) (the mask's
-    -inf entries drop out), in float64 from the fp16 operands; a row with no
-    visible key gives 0. The fused pass of attention-fa.comp (scores at
-    :581-591, online softmax, P.V), /root/reference/vai/shaders/."""
+def attention(q, k, v, *, scale=None, causal=False, span=0, out_dtype=np.float32, blocks=None):
+    """The reference's Attention node without a KV cache: O[..., i, h, :] =
+    sum_j softmax_j(S[..., h, i, :]) V[..., h / g, j, :], S = attn_scores(q, k)
+    (the mask's -inf entries drop out), evaluated in float64 from the
+    operands' exact values. Q [..., Hq, Tq, D], K / V [..., Hkv, Tkv, D], each
+    fp32 or fp16; O is token-major [..., Tq, Hq, D]
+    (/root/reference/vai/shaders/attention-fa.comp:8,96; nodes/attention.h:
+    1220-1223). No mask unless one is asked for (attention.h:129: a null mask
+    binds no mask); a row with no visible key gives 0 (attention-fa.comp:889).
+    The fused pass of attention-fa.comp (scores at :581-591, online softmax,
+    P.V); this restatement takes the exact softmax, the limit that the
+    reference's fp32 sweep approximates."""
     q, k, v = _c(q), _c(k), _c(v)
+    if q.dtype != k.dtype:   # the scores oracle reads one dtype: fp32 holds fp16 values exactly
+        q, k = q.astype(np.float32), k.astype(np.float32)
     S = attn_scores(q, k, scale=scale, causal=causal, span=span, blocks=blocks).astype(np.float64)
     Hq, Tq, D = q.shape[-3:]
     Hkv, Tkv, _ = k.shape[-3:]
@@ -220,8 +229,8 @@ def attention(q, k, v, *, scale=None, causal=True, span=0, out_dtype=np.float32,
     P = np.where(finite, np.exp(S - m), 0.0)
     l = P.sum(axis=-1, keepdims=True)
     O = np.einsum("...ij,...jd->...id", P, vv)
-    O = np.where(l > 0, O / np.where(l > 0, l, 1.0), 0.0)
-    return O.astype(out_dtype)
+    O = np.where(l > 0, O / np.where(l > 0, l, 1.0), 0.0)   # [..., Hq, Tq, D]
+    return np.ascontiguousarray(np.swapaxes(O, -3, -2)).astype(out_dtype)
 
 
 # ---- CPU baseline (cpu_baseline.c): the timed CPU restatement bench.py reports ----

@@ -236,7 +236,7 @@ static float acc16_span(const uint16_t* a, const uint16_t* b, uint32_t k0, uint3
             sum = orc_fma16(kk < k1 ? a[kk] : 0, kk < k1 ? b[kk] : 0, sum);
         }
     const float v = orc_h2f(sum);
-    return fminf(fmaxf(v, -65504.f), 65504.f);
+    return v != v ? v : fminf(fmaxf(v, -65504.f), 65504.f);   /* a NaN chain stays NaN */
 }
 
 /* O = s*epi(sum_z P_z + B) (+R), P_z the fp16-accumulated split sums; gated:

@@ -71,3 +71,24 @@ def test_acc16_where_the_reference_keeps_fp32(gpu):
     x = draw((4, 256), rng, np.float16)
     w = draw(normal((64, 256), 0.05), rng, np.float16)
     assert_close(run_linear(gpu, x, w, acc=np.float16), oracle.linear(x, w, stage="slab"), (1e-5, 1e-6))
+
+
+@pytest.mark.parametrize("m, k, n, want_splits", [
+    (64, 4096, 64, 8),     # one 64x64 tile: 8 spans of 512, each its own fp16 chain
+    (130, 2304, 260, 5),   # 6 tiles of 128: 8-6 splits leave the last span empty, 5 do not
+])
+def test_acc16_auto_split_bit_exact(gpu, m, k, n, want_splits):
+    """splitSize 0 with K >= 2048 on an underfilled grid: the reference splits
+    K by ggmlGuessSplitCount (linear.h:600-632) and so does the plan; the sums
+    match the oracle's chains over the same 256-rounded spans bit for bit."""
+    rng = np.random.default_rng(k)
+    w = draw(normal((n, k), 0.02), rng, np.float16)
+    x = draw((m, k), rng, np.float16)
+    args = gpu.linear_args(gpu.DeviceArray((m, n), np.float32), gpu.DeviceArray((m, k), np.float16),
+                           gpu.DeviceArray((n, k), np.float16), acc=np.float16)
+    assert gpu.linear_plan(args)[1] == want_splits
+    span = -(-(-(-k // want_splits)) // 256) * 256
+    got = run_linear(gpu, x, w, acc=np.float16)
+    want = oracle.linear_acc16(x, w, split_size=span)
+    assert np.array_equal(got, want), f"{(got != want).sum()} outputs differ"
+    assert not np.array_equal(got, oracle.linear_acc16(x, w))   # one chain over all of K differs

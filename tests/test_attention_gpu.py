@@ -1,11 +1,16 @@
-"""Fused attention forward (scores, online softmax, P.V in one kernel)
-through the C ABI vs the oracle's float64 softmax(S) V. The reference's
-Attention node (/root/reference/vai/nodes/attention.h:979-1304, shaders/
-attention-fa.comp) with its causal / sliding-window rule (common/
-causal_mask.h:25-42), GQA, Tq != Tkv, head dims 64/128/256, tails.
-P enters the P.V product as fp16 (as the reference's fp16 P.V operand), so
-the comparison uses the fp16 tier.
+"""Attention forward through the C ABI vs the oracle's float64 softmax(S) V.
+The reference's Attention node (/root/reference/vai/nodes/attention.h:77-129,
+979-1304, shaders/attention-fa.comp, attention.comp): O token-major
+[B, Tq, Hq, D], no mask unless one is set, Q and K / V each fp32 or fp16, any
+head dim; the causal / sliding-window / block rule of common/causal_mask.h:
+25-42, GQA, Tq != Tkv, tails. The flash kernel computes Q.K^T and P.V on
+fp16 operands (fp32 Q / K / V rounded to fp16, P rounded to fp16, as the
+reference's f16-staged tiles and fp16 P.V operand), so it is held to the
+fp16 tier; the plain fp32 kernel (head dims the flash kernel does not take)
+to a tighter one.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -34,13 +39,13 @@ def test_attention(gpu, b, hq, hkv, tq, tkv, d, causal, span, odt):
     k = draw((b, hkv, tkv, d), rng, np.float16)
     v = draw((b, hkv, tkv, d), rng, np.float16)
     D = gpu.DeviceArray.from_numpy
-    out = gpu.DeviceArray((b, hq, tq, d), odt)
+    out = gpu.DeviceArray((b, tq, hq, d), odt)
     print(f"attention b={b} hq={hq} hkv={hkv} tq={tq} tkv={tkv} d={d} causal={causal} span={span}", flush=True)
     got = gpu.attention(out, D(q), D(k), D(v), causal=causal, span=span).numpy().astype(np.float32)
     want = oracle.attention(q, k, v, causal=causal, span=span, out_dtype=np.float32)
     assert_close(got, want, FP16)
     if causal and tq > tkv:
-        np.testing.assert_array_equal(got[..., : tq - tkv, :], 0.0)
+        np.testing.assert_array_equal(got[:, : tq - tkv], 0.0)
 
 
 @pytest.mark.parametrize("hq, hkv, tq, tkv, d, blocks, span", [
@@ -55,23 +60,85 @@ def test_attention_block_mask(gpu, hq, hkv, tq, tkv, d, blocks, span):
     k = draw((1, hkv, tkv, d), rng, np.float16)
     v = draw((1, hkv, tkv, d), rng, np.float16)
     D = gpu.DeviceArray.from_numpy
-    out = gpu.DeviceArray((1, hq, tq, d), np.float32)
+    out = gpu.DeviceArray((1, tq, hq, d), np.float32)
     print(f"attention blocks={blocks} hq={hq} hkv={hkv} tq={tq} tkv={tkv} d={d} span={span}", flush=True)
     got = gpu.attention(out, D(q), D(k), D(v), blocks=blocks, span=span).numpy()
     want = oracle.attention(q, k, v, blocks=blocks, span=span, out_dtype=np.float32)
     assert_close(got, want, FP16)
 
 
+NAIVE = (1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("b, hq, hkv, tq, tkv, d, qdt, kvdt, odt, causal", [
+    (1, 16, 16, 729, 729, 72, np.float32, np.float32, np.float32, False),   # SigLIP's encoder attention (Dh 72)
+    (2, 4, 2, 100, 100, 72, np.float16, np.float16, np.float16, True),      # Dh 72 in fp16, GQA, causal
+    (1, 8, 2, 130, 300, 128, np.float32, np.float16, np.float32, True),     # fp32 Q over fp16 K / V (Linear -> cache dtype)
+    (1, 4, 4, 64, 1000, 64, np.float16, np.float32, np.float16, False),     # fp32 K / V: fp16 copies, key split
+    (1, 2, 1, 50, 50, 16, np.float32, np.float32, np.float32, True),        # smallest flash head dim
+    (1, 2, 2, 70, 90, 200, np.float32, np.float16, np.float32, False),      # Dh 200: padded to 256
+    (1, 3, 3, 40, 40, 40, np.float16, np.float16, np.float32, True),        # Dh 40: padded to 64
+])
+def test_attention_dtypes_and_head_dims(gpu, b, hq, hkv, tq, tkv, d, qdt, kvdt, odt, causal):
+    rng = np.random.default_rng(d + tq)
+    q = draw((b, hq, tq, d), rng, qdt)
+    k = draw((b, hkv, tkv, d), rng, kvdt)
+    v = draw((b, hkv, tkv, d), rng, kvdt)
+    D = gpu.DeviceArray.from_numpy
+    out = gpu.DeviceArray((b, tq, hq, d), odt)
+    print(f"attention b={b} hq={hq} hkv={hkv} tq={tq} tkv={tkv} d={d} q={qdt.__name__} kv={kvdt.__name__}",
+          flush=True)
+    got = gpu.attention(out, D(q), D(k), D(v), causal=causal).numpy().astype(np.float32)
+    assert_close(got, oracle.attention(q, k, v, causal=causal, out_dtype=np.float32), FP16)
+
+
+@pytest.mark.parametrize("b, hq, hkv, tq, tkv, d, qdt, kvdt, causal, span", [
+    (1, 2, 1, 33, 47, 20, np.float32, np.float32, True, 0),     # Dh % 8 != 0: the plain kernel
+    (2, 2, 2, 17, 17, 8, np.float16, np.float16, False, 0),     # Dh < 16
+    (1, 2, 2, 40, 300, 300, np.float32, np.float16, True, 100),  # Dh > 256, window, more keys than a tile
+    (1, 1, 1, 9, 3, 12, np.float16, np.float32, True, 0),       # queries with no visible key give 0
+])
+def test_attention_plain_kernel(gpu, b, hq, hkv, tq, tkv, d, qdt, kvdt, causal, span):
+    rng = np.random.default_rng(d)
+    q = draw((b, hq, tq, d), rng, qdt)
+    k = draw((b, hkv, tkv, d), rng, kvdt)
+    v = draw((b, hkv, tkv, d), rng, kvdt)
+    D = gpu.DeviceArray.from_numpy
+    out = gpu.DeviceArray((b, tq, hq, d), np.float32)
+    a = gpu.attention_args(out, D(q), D(k), D(v), causal=causal, span=span)
+    assert gpu.lib().vai_attention_workspace_size(ctypes.byref(a)) == 0
+    print(f"attention plain b={b} hq={hq} tq={tq} tkv={tkv} d={d} span={span}", flush=True)
+    got = gpu.attention(out, D(q), D(k), D(v), causal=causal, span=span).numpy()
+    assert_close(got, oracle.attention(q, k, v, causal=causal, span=span, out_dtype=np.float32), NAIVE)
+
+
+def test_attention_layout_and_no_mask_default(gpu):
+    """The output is token-major: the independent head-major float64 result
+    transposed by numpy (Tq, Hq and D all distinct). Without a mask argument
+    every query attends every key (attention.h:129), on both kernels."""
+    rng = np.random.default_rng(21)
+    for d in (72, 36):
+        q = draw((2, 3, 40, d), rng, np.float32)
+        k = draw((2, 3, 56, d), rng, np.float32)
+        v = draw((2, 3, 56, d), rng, np.float32)
+        s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), k.astype(np.float64)) / np.sqrt(d)
+        p = np.exp(s - s.max(-1, keepdims=True))
+        head_major = np.einsum("bhij,bhjd->bhid", p / p.sum(-1, keepdims=True), v.astype(np.float64))
+        D = gpu.DeviceArray.from_numpy
+        print(f"attention layout d={d}", flush=True)
+        got = gpu.attention(gpu.DeviceArray((2, 40, 3, d), np.float32), D(q), D(k), D(v)).numpy()
+        assert_close(got, np.transpose(head_major, (0, 2, 1, 3)), FP16)
+
+
 def test_attention_rejects(gpu):
-    """fp32 inputs and head dims other than 64/128/256 are refused."""
-    import ctypes
+    """A dtype other than fp32 / fp16 and a zero head dim are refused."""
     D = gpu.DeviceArray
     a = gpu.attention_args(D((1, 1, 8, 64), np.float32), D((1, 1, 8, 64), np.float32), D((1, 1, 8, 64), np.float32),
                            D((1, 1, 8, 64), np.float32))
+    a.kv_dtype = 5
     assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1003
-    a = gpu.attention_args(D((1, 1, 8, 96), np.float32), D((1, 1, 8, 96), np.float16), D((1, 1, 8, 96), np.float16),
-                           D((1, 1, 8, 96), np.float16))
-    assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1005
+    a.kv_dtype, a.head_dim = 0, 0
+    assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1002
 
 
 def test_attention_workspace(gpu):

@@ -81,3 +81,56 @@ def test_plans():
     assert splits == 4
     name, splits = plan(2048, 16384, 3072, gated=1, gate_epilogue=4)
     assert name.endswith("_gated") and splits == 1
+
+
+def test_acc16_auto_split_follows_the_reference():
+    """An fp16-accumulating Linear with splitSize 0 splits K as the reference's
+    ggmlGuessSplitCount does for its scalar tile (linear.h:600-632): each
+    split starts its own fp16 chain, so the count changes the sums. Counts
+    below are worked by hand from that rule for 256 compute units."""
+    def plan(m, n, k, split_size=0):
+        a = _capi.LinearArgs()
+        a.out = a.inp = a.weight = 256
+        a.M, a.N, a.K = m, n, k
+        a.o_dtype, a.i_dtype, a.w_dtype = 0, 1, 1
+        a.acc_dtype = 1
+        a.scalar_scale = 1.0
+        a.split_size = split_size
+        return _capi.linear_plan(a)
+    # 64x64: the M tier (64x64 tiles), 1 tile <= 128 -> min(256, 8) = 8 spans of 512
+    assert plan(64, 64, 4096)[1] == 8
+    # K < 2048: never split
+    assert plan(64, 64, 2047)[1] == 1
+    # 256x256 (L tier, 128x128): 4 tiles -> 8 splits; K = 2048: spans of 256, 8 * 256 - 256 < 2048
+    assert plan(256, 256, 2048)[1] == 8
+    # K = 2304: 8, 7 and 6 splits all round to spans of 512 that leave the last split empty
+    # (7, 6, 5 x 512 >= 2304); 5 splits: span 512, 4 x 512 = 2048 < 2304
+    assert plan(256, 256, 2304)[1] == 5
+    # 2048 x 2048: 256 tiles of 128 > 256 * 2 / 3: no split
+    assert plan(2048, 2048, 4096)[1] == 1
+    # 1536 x 1536: 144 tiles, > 128 but <= 170: 3 splits
+    assert plan(1536, 1536, 4096)[1] == 3
+    # N below the tile: no split (ggml's N < wgN gate); M, N <= 32: S tier 32x32
+    assert plan(64, 16, 4096)[1] == 1
+    # an explicit span wins
+    assert plan(64, 64, 4096, split_size=1024)[1] == 4
+
+
+def test_attention_argument_checks_need_no_gpu():
+    """bf16-like dtype codes and zero sizes are refused; any head dim passes
+    the checks (the plain kernel takes what the flash kernel cannot)."""
+    lib = _capi.lib()
+    a = _capi.AttentionArgs()
+    a.out = a.q = a.k = a.v = 256
+    a.batch, a.hq, a.hkv, a.tq, a.tkv, a.head_dim = 1, 2, 1, 4, 4, 72
+    a.q_dtype, a.kv_dtype, a.o_dtype = 0, 7, 0
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1003
+    a.kv_dtype = 0
+    a.head_dim = 0
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1002
+    # fp32 K / V at a flash head dim need fp16 copies: 2 x (4 x 72) x 2 = 1152 bytes, rounded to 1280
+    a.head_dim = 72
+    assert lib.vai_attention_workspace_size(ctypes.byref(a)) == 1280
+    # fp16 K / V at head dim 20 (not a multiple of 8): the plain kernel, no workspace
+    a.head_dim, a.kv_dtype = 20, 1
+    assert lib.vai_attention_workspace_size(ctypes.byref(a)) == 0

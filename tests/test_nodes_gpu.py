@@ -157,22 +157,41 @@ def test_attention_scores_node(gpu, hq, hkv, tq, tkv, d, causal):
     assert_close(got, oracle.attn_scores(q, k, causal=causal), FP32)
 
 
-@pytest.mark.parametrize("hq, hkv, tq, tkv, d, causal, span", [(4, 2, 100, 100, 128, True, 0),
-                                                               (2, 2, 64, 1000, 64, False, 0),
-                                                               (2, 1, 257, 257, 64, True, 50)])
-def test_attention_node(gpu, hq, hkv, tq, tkv, d, causal, span):
-    """The engine's Attention node (Q, K, V -> out0) runs the fused kernel,
-    binding its key-split partials to the "partialO" temporary when the
-    launch splits key ranges (the 1000-key case)."""
+@pytest.mark.parametrize("hq, hkv, tq, tkv, d, causal, span, qdt, kvdt", [
+    (4, 2, 100, 100, 128, True, 0, np.float16, np.float16),
+    (2, 2, 64, 1000, 64, False, 0, np.float16, np.float16),
+    (2, 1, 257, 257, 64, True, 50, np.float16, np.float16),
+    (16, 16, 729, 729, 72, False, 0, np.float32, np.float32),   # SigLIP: Dh 72, fp32 Linear outputs, no mask
+    (4, 2, 90, 90, 128, True, 0, np.float32, np.float16),       # fp32 Q, K / V in the cache dtype
+    (2, 2, 30, 30, 20, True, 0, np.float32, np.float32),        # Dh 20: the plain kernel
+])
+def test_attention_node(gpu, hq, hkv, tq, tkv, d, causal, span, qdt, kvdt):
+    """The engine's Attention node (Q, K, V -> out0 [..., Tq, Hq, D]) with the
+    reference's Config and setCausalMask; the key-split partials and fp16
+    K / V copies bind to the "partialO" temporary when the launch needs them."""
     pv = pyvai()
     rng = np.random.default_rng(3)
-    q = draw((1, hq, tq, d), rng, np.float16)
-    k = draw((1, hkv, tkv, d), rng, np.float16)
-    v = draw((1, hkv, tkv, d), rng, np.float16)
-    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d, num_kv_heads=hkv, causal=causal,
-                                                   span=span), ["Q", "K", "V"], {})
+    q = draw((1, hq, tq, d), rng, qdt)
+    k = draw((1, hkv, tkv, d), rng, kvdt)
+    v = draw((1, hkv, tkv, d), rng, kvdt)
+    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d, num_kv_heads=hkv), ["Q", "K", "V"], {})
+    if causal or span:
+        net.node.set_causal_mask(1 if causal else 0, [], span=span)
     got = forward(net, {"Q": q, "K": k, "V": v}).astype(np.float32)
+    assert got.shape == (1, tq, hq, d)
     assert_close(got, oracle.attention(q, k, v, causal=causal, span=span, out_dtype=np.float32), FP16)
+
+
+def test_attention_node_no_mask_by_default(gpu):
+    """Without setCausalMask every query attends every key (attention.h:129):
+    the first query's output is not V's first row."""
+    pv = pyvai()
+    rng = np.random.default_rng(8)
+    q, k, v = (draw((1, 2, 40, 64), rng, np.float16) for _ in range(3))
+    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=2, head_dim=64), ["Q", "K", "V"], {})
+    got = forward(net, {"Q": q, "K": k, "V": v}).astype(np.float32)
+    assert_close(got, oracle.attention(q, k, v, out_dtype=np.float32), FP16)
+    assert not np.allclose(got[0, 0, 0], v[0, 0, 0], atol=1e-2)
 
 
 def test_attention_node_block_mask(gpu):

@@ -238,10 +238,21 @@ def _attn_inputs(rng, hq, hkv, tq, tkv, d):
     return q, k, v
 
 
+def _np_attention_head_major(q, k, v, scale):
+    """float64 softmax(q k^T scale) v per head with no mask, head-major
+    [B, Hq, Tq, D], written with numpy alone (no oracle code)."""
+    q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
+    g = q.shape[1] // k.shape[1]
+    k, v = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    s = np.einsum("bhid,bhjd->bhij", q, k) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return np.einsum("bhij,bhjd->bhid", p / p.sum(-1, keepdims=True), v)
+
+
 def test_attention_oracle_pins():
     """oracle.attention composes the pinned scores with softmax and P.V;
     these properties fail for a dropped normalisation, a reversed mask or a
-    transposed V."""
+    transposed V. O is token-major: o[b, i, h] is query i of head h."""
     rng = np.random.default_rng(0)
     q, k, v = _attn_inputs(rng, 2, 1, 5, 7, 8)
     # V of ones: every row with a visible key returns exactly 1
@@ -250,27 +261,52 @@ def test_attention_oracle_pins():
     # V = identity rows (Tkv = D): O is the softmax matrix itself
     q2, k2, _ = _attn_inputs(rng, 1, 1, 6, 8, 8)
     eye = np.eye(8, dtype=np.float16)[None, None]
-    o = oracle.attention(q2, k2, eye, causal=False, out_dtype=np.float64)[0, 0]
+    o = oracle.attention(q2, k2, eye, causal=False, out_dtype=np.float64)[0, :, 0]
     s = q2[0, 0].astype(np.float64) @ k2[0, 0].astype(np.float64).T / np.sqrt(8)
     p = np.exp(s - s.max(1, keepdims=True))
     np.testing.assert_allclose(o, p / p.sum(1, keepdims=True), rtol=1e-6)
     # causal with Tq = Tkv: query 0 sees key 0 alone, so O[0] = V[0]; the
     # last query sees every key
     q3, k3, v3 = _attn_inputs(rng, 1, 1, 6, 6, 8)
-    o = oracle.attention(q3, k3, v3, causal=True, out_dtype=np.float64)[0, 0]
+    o = oracle.attention(q3, k3, v3, causal=True, out_dtype=np.float64)[0, :, 0]
     np.testing.assert_array_equal(o[0], v3[0, 0, 0].astype(np.float64))
-    full = oracle.attention(q3, k3, v3, causal=False, out_dtype=np.float64)[0, 0]
+    full = oracle.attention(q3, k3, v3, causal=False, out_dtype=np.float64)[0, :, 0]
     np.testing.assert_allclose(o[-1], full[-1], rtol=1e-12)
     # GQA: two query heads over one K/V head equal two single-head calls
     qa, kb, vb = _attn_inputs(rng, 2, 1, 4, 4, 8)
     both = oracle.attention(qa, kb, vb, causal=True, out_dtype=np.float64)
     for h in range(2):
         one = oracle.attention(qa[:, h:h + 1], kb, vb, causal=True, out_dtype=np.float64)
-        np.testing.assert_allclose(both[:, h:h + 1], one, rtol=1e-12)
+        np.testing.assert_allclose(both[:, :, h:h + 1], one, rtol=1e-12)
     # Tq > Tkv under the causal rule: the first queries see no key and give 0
     q4, k4, v4 = _attn_inputs(rng, 1, 1, 5, 3, 8)
-    o = oracle.attention(q4, k4, v4, causal=True, out_dtype=np.float64)[0, 0]
+    o = oracle.attention(q4, k4, v4, causal=True, out_dtype=np.float64)[0, :, 0]
     np.testing.assert_array_equal(o[:2], 0.0)
+
+
+def test_attention_oracle_layout_and_defaults():
+    """The reference's contract (attention.h:77-79,129; attention-fa.comp:96):
+    out0 is [B, Tq, Hq, D] -- the independent head-major float64 result
+    transposed by numpy -- and no mask applies unless one is asked for.
+    Distinct Tq, Hq and D (and Hq != Hkv) make a wrong axis order fail."""
+    rng = np.random.default_rng(11)
+    q, k, v = _attn_inputs(rng, 4, 2, 5, 9, 24)
+    want = np.transpose(_np_attention_head_major(q, k, v, 1 / np.sqrt(24)), (0, 2, 1, 3))
+    got = oracle.attention(q, k, v, out_dtype=np.float64)
+    assert got.shape == (1, 5, 4, 24)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    causal = oracle.attention(q, k, v, causal=True, out_dtype=np.float64)
+    assert not np.allclose(causal, got)
+    # fp32 Q with fp16 K / V (the reference's typeI / typeKV, attention.h:86-88)
+    q32 = rng.standard_normal(q.shape).astype(np.float32)
+    got = oracle.attention(q32, k, v, out_dtype=np.float64)
+    want = np.transpose(_np_attention_head_major(q32, k, v, 1 / np.sqrt(24)), (0, 2, 1, 3))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    # fp32 everything, head dim 72 (SigLIP's, /root/reference/models/common.h:30)
+    q, k, v = (rng.standard_normal((2, 3, 7, 72)).astype(np.float32) for _ in range(3))
+    got = oracle.attention(q, k, v, out_dtype=np.float64)
+    want = np.transpose(_np_attention_head_major(q, k, v, 1 / np.sqrt(72)), (0, 2, 1, 3))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
 
 
 # ---- fp16 accumulation (Linear::setAccDtype(Fp16), linear-tile.comp:292-320) --
@@ -417,3 +453,19 @@ def test_scores_block_masks(tq, tkv, blocks, ends_per_row):
     lo = np.where(pos >= 2, pos - 1, 0)
     vis2 = vis & (np.arange(tkv)[None, :] >= lo[:, None])
     assert np.array_equal(np.isfinite(got[0]), vis2)
+
+
+def test_acc16_nan_chain_stays_nan():
+    """The fp16 accumulator's clamp to +-65504 keeps a NaN sum NaN (GLSL
+    leaves clamp of a NaN undefined; a finite clamp would hide the fault), and
+    still clamps an overflowed chain: a row that overflows to +inf and then
+    meets -inf gives NaN, a row that only overflows gives 65504."""
+    x = np.zeros((2, 8), np.float16)
+    w = np.zeros((1, 8), np.float16)
+    w[0, :] = 1
+    x[0, 0], x[0, 4] = 60000, np.float16(np.inf)     # an overflowing chain ...
+    x[0, 1] = -np.float16(np.inf)                     # ... meets -inf: NaN
+    x[1, :2] = 60000                                  # 120000 overflows to +inf: clamped
+    out = oracle.linear_acc16(x, w)
+    assert np.isnan(out[0, 0])
+    assert out[1, 0] == 65504.0

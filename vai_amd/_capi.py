@@ -76,7 +76,7 @@ class AttnScoresArgs(ctypes.Structure):
 class AttentionArgs(ctypes.Structure):
     _fields_ = [
         ("out", ctypes.c_void_p), ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
-        ("o_dtype", ctypes.c_int32), ("i_dtype", ctypes.c_int32),
+        ("o_dtype", ctypes.c_int32), ("q_dtype", ctypes.c_int32), ("kv_dtype", ctypes.c_int32),
         ("batch", ctypes.c_uint32), ("hq", ctypes.c_uint32), ("hkv", ctypes.c_uint32),
         ("tq", ctypes.c_uint32), ("tkv", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
         ("scale", ctypes.c_float), ("causal", ctypes.c_uint32), ("span", ctypes.c_uint32),
@@ -369,12 +369,13 @@ def attn_scores(scores, q, k, stream=None, **kw):
     return scores
 
 
-def attention_args(out, q, k, v, *, scale=None, causal=True, span=0, blocks=None):
+def attention_args(out, q, k, v, *, scale=None, causal=False, span=0, blocks=None):
+    """O token-major [..., Tq, Hq, D]; no mask unless causal / blocks ask for one."""
     Hq, Tq, D = q.shape[-3:]
     Hkv, Tkv, _ = k.shape[-3:]
     a = AttentionArgs()
     a.out, a.q, a.k, a.v = out.ptr, q.ptr, k.ptr, v.ptr
-    a.o_dtype, a.i_dtype = out.code, q.code
+    a.o_dtype, a.q_dtype, a.kv_dtype = out.code, q.code, k.code
     a.batch = int(np.prod(q.shape[:-3]))
     a.hq, a.hkv, a.tq, a.tkv, a.head_dim = Hq, Hkv, Tq, Tkv, D
     a.scale = 0.0 if scale is None else float(scale)

@@ -203,23 +203,24 @@ __host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt)
     return n <= 0 ? 1u : ((uint32_t)n + p.chunk_tiles - 1) / p.chunk_tiles;
 }
 
-// K / V tile copies of key rows [row0, row0 + 64) into stage t % 2: copy j
-// of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB); rows past Tkv
-// read as zero (buffer range check).
+// K / V tile copies of the 64 key rows from byte soff of the head into stage
+// t % 2: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
+// rows past Tkv and the padding past the head dim read as zero (buffer range
+// check).
 template <int D>
 __device__ __forceinline__ void fa_issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, LDS_AS char* lds,
-                                         const uint32_t* coff, int row0, int t, int wave)
+                                         const uint32_t* coff, int soff, int t, int wave)
 {
     using L = fa::Lds<D>;
     LDS_AS char* st = lds + (t & 1) * L::STAGE + wave * L::COPIES * 1024;
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(st + j * 1024), 16, (int)coff[j],
-                                                 row0 * L::ROWB, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(st + j * 1024), 16, (int)coff[j], soff, 0,
+                                                 0);
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(st + L::TILE + j * 1024), 16, (int)coff[j],
-                                                 row0 * L::ROWB, 0, 0);
+                                                 soff, 0, 0);
 }
 
 template <int N>
@@ -229,11 +230,16 @@ __device__ __forceinline__ void fa_wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// D is the padded head dim the LDS tiles and MFMA steps use (64, 128 or
+// 256); HD = p.head_dim <= D is the operands' own, a multiple of 8. The
+// padding reads as zero (out of the buffers' range), so it adds nothing to
+// any score or output; output columns past HD are not stored.
 template <int D>
 __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 {
     using namespace fa;
     using L = Lds<D>;
+    const uint32_t HD = p.head_dim, ROWG = HD * 2;   // head dim and K / V row bytes in HBM
     constexpr int KS = D / 16, DF = D / 32;   // 16-wide head-dim steps; 32-wide output fragments
     extern __shared__ half8 fa_lds[];
     LDS_AS char* lds = (LDS_AS char*)(LDS_AS void*)fa_lds;
@@ -273,7 +279,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     }
     const uint32_t q0 = qt * BQ;
     const uint32_t hk = h / (p.hq / p.hkv);
-    const half_t* Q = (const half_t*)p.q + ((size_t)b * p.hq + h) * Tq * D;
+    const uint32_t qsz = p.q_dtype == DT_F32 ? 4 : 2;
+    const char* Q = (const char*)p.q + ((size_t)b * p.hq + h) * Tq * HD * qsz;
 
     const uint32_t qrow = q0 + wave * QW + ql;
 
@@ -290,21 +297,22 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // K / V tile copies: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
     // lane l's 16 bytes land at physical chunk pc of row r and come from
     // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
+    // (a chunk past the head dim points at byte 2^31, beyond any range)
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * D), (short)0, (int)((size_t)Tkv * D * 2),
+        (void*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD), (short)0, (int)(Tkv * ROWG),
         0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * D), (short)0, (int)((size_t)Tkv * D * 2),
+        (void*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD), (short)0, (int)(Tkv * ROWG),
         0x00020000);
     uint32_t coff[L::COPIES];
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j) {
         const int byte = (wave * L::COPIES + j) * 1024 + lane * 16;
-        const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16;
-        coff[j] = (uint32_t)(r * L::ROWB + swz<D>(r, pc) * 16);
+        const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16, lc = swz<D>(r, pc);
+        coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
     }
     const auto issue = [&](int t) __attribute__((always_inline)) {
-        fa_issue<D>(rk, rv, lds, coff, (int)(tb + t) * BKV, t, wave);
+        fa_issue<D>(rk, rv, lds, coff, (int)((tb + t) * BKV * ROWG), t, wave);
     };
 
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
@@ -341,14 +349,30 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // 1 is in flight during the prologue. Vector loads and the LDS copies
     // each complete in issue order, so once at most the tile-1 copies are
     // outstanding, the query rows and tile 0 have landed.
+    // fp32 Q is rounded to fp16 here (the reference's f16 staging of Q,
+    // attention-fa.comp:335-342 with stagingF16, as its AMD tiles take).
     half8 qf[KS];
     {
         const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(Q + (size_t)q0 * D), (short)0, (int)((size_t)(Tq - q0) * D * 2), 0x00020000);
-        const uint32_t qoff = (uint32_t)((wave * QW + ql) * D + 8 * hf) * 2;
+            (void*)(Q + (size_t)q0 * HD * qsz), (short)0, (int)((Tq - q0) * HD * qsz), 0x00020000);
+        const uint32_t qel = (wave * QW + ql) * HD + 8 * hf;   // first element of step 0
+        if (p.q_dtype == DT_F32) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-            qf[s] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(qoff + 32 * s), 0, 0));
+            for (int s = 0; s < KS; ++s) {
+                const uint32_t off = 16 * s + 8 * hf < HD ? (qel + 16 * s) * 4 : 0x80000000u;
+                const float4v lo = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)off, 0, 0));
+                const float4v hi =
+                    __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)off, 16, 0));
+                const half4 l4 = __builtin_convertvector(lo, half4), h4 = __builtin_convertvector(hi, half4);
+                qf[s] = __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const uint32_t off = 16 * s + 8 * hf < HD ? (qel + 16 * s) * 2 : 0x80000000u;
+                qf[s] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)off, 0, 0));
+            }
+        }
     }
     if (ntiles > 0) issue(0);
     if (ntiles > 1) {
@@ -540,18 +564,19 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         wml[0] = m;
         wml[1] = l;
     }
+    // Partials keep the padded rows (D wide); the output is token-major
+    // [batch, Tq, Hq, HD]: query row r of head h at row (b Tq + r) Hq + h.
     const uint32_t wrow0 = q0 + wave * QW;   // the wave's first query row
-    const size_t row0 = partial ? gid * BQ + wave * QW : ((size_t)b * p.hq + h) * Tq + wrow0;
 #pragma unroll
     for (int j = 0; j < QW * CR / 64; ++j) {
         const int e = j * 64 + lane, r = e / CR, c = e % CR;
         const float4v v = ob[r * CR + (c ^ (r & 15))];
-        const size_t o0 = (row0 + r) * D + 4 * c;
-        if (part16) {
-            *(half4*)((half_t*)p.ws_o + o0) = __builtin_convertvector(v, half4);
-        } else if (partial) {
-            *(float4v*)(p.ws_o + o0) = v;
-        } else if (wrow0 + r < Tq) {
+        if (partial) {
+            const size_t o0 = (gid * BQ + wave * QW + r) * D + 4 * c;
+            if (part16) *(half4*)((half_t*)p.ws_o + o0) = __builtin_convertvector(v, half4);
+            else *(float4v*)(p.ws_o + o0) = v;
+        } else if (wrow0 + r < Tq && 4u * c < HD) {
+            const size_t o0 = (((size_t)b * Tq + wrow0 + r) * p.hq + h) * HD + 4 * c;
             if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o0) = __builtin_convertvector(v, half4);
             else *(float4v*)((float*)p.out + o0) = v;
         }
@@ -612,7 +637,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
     const uint32_t ncr = (nc + 7) & ~7u;
     for (uint32_t e = threadIdx.x * 4; e < RG * D; e += 256 * 4) {
         const uint32_t rl = e / D, col = e % D, qrow = qt * BQ + r0 + rl;
-        if (qrow >= p.tq) continue;
+        if (qrow >= p.tq || col >= p.head_dim) continue;   // (whole 4-column groups: head_dim % 8 == 0)
         const size_t base = (g0 * BQ + r0 + rl) * D + col, cstride = (size_t)BQ * D;
         float4v acc = (float4v)0.f;
         if (part16) {
@@ -634,7 +659,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
                 for (int i = 0; i < 8; ++i) acc += wgt[rl][c0 + i] * v[i];
             }
         }
-        const size_t o = (((size_t)b * p.hq + h) * p.tq + qrow) * D + col;
+        const size_t o = (((size_t)b * p.tq + qrow) * p.hq + h) * p.head_dim + col;
         if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(acc, half4);
         else *(float4v*)((float*)p.out + o) = acc;
     }
@@ -650,16 +675,113 @@ uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles)
     return units == nqt ? 0u : units;
 }
 
+// The plain path: one workgroup per (query row, head, sequence) walks the
+// row's visible keys 256 at a time in fp32 -- thread t scores key j0 + t,
+// the block takes the tile's max and sum (online softmax in natural-log
+// units, as attention.comp's fp32 naive kernel), then every thread adds the
+// tile's P V into the head-dim columns it owns (t, t + 256, ..). Any head dim
+// up to 256 * NAIVE_COLS, any mix of fp32 / fp16 operands; no workspace.
+constexpr int NAIVE_COLS = 8;
+
+__device__ __forceinline__ float naive_block_reduce(float v, bool is_max, float* red)
+{
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        const float o = __shfl_xor(v, s, 64);
+        v = is_max ? fmaxf(v, o) : v + o;
+    }
+    __syncthreads();   // red's previous readers are done
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
+    return v;
+}
+
+__global__ __launch_bounds__(256) void attention_naive_kernel(AttnParams p)
+{
+    __shared__ float qs[256 * NAIVE_COLS];
+    __shared__ float ps[256];
+    __shared__ float red[4];
+    const uint32_t i = blockIdx.x, h = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
+    const uint32_t HD = p.head_dim, hk = h / (p.hq / p.hkv);
+    const size_t qbase = (((size_t)b * p.hq + h) * p.tq + i) * HD;
+    const size_t kvbase = ((size_t)b * p.hkv + hk) * p.tkv * HD;
+    for (uint32_t d = t; d < HD; d += 256) qs[d] = ld(p.q, p.q_dtype, qbase + d);
+    const int64_t kbeg = p.mask.key_start(i), kend = p.mask.key_end(i);
+    float o[NAIVE_COLS];
+#pragma unroll
+    for (int r = 0; r < NAIVE_COLS; ++r) o[r] = 0.f;
+    float m = -__builtin_inff(), l = 0.f;
+    __syncthreads();
+    for (int64_t j0 = kbeg; j0 < kend; j0 += 256) {
+        const int64_t j = j0 + t;
+        float sc = -__builtin_inff();
+        if (j < kend) {
+            float acc = 0.f;
+            for (uint32_t d = 0; d < HD; ++d) acc = fmaf(qs[d], ld(p.k, p.kv_dtype, kvbase + (size_t)j * HD + d), acc);
+            sc = acc * p.scale;
+        }
+        const float mnew = fmaxf(m, naive_block_reduce(sc, true, red));   // finite: the tile has a key
+        const float alpha = m == -__builtin_inff() ? 0.f : expf(m - mnew);
+        const float e = sc == -__builtin_inff() ? 0.f : expf(sc - mnew);
+        ps[t] = e;
+        l = l * alpha + naive_block_reduce(e, false, red);   // (its barriers publish ps)
+        m = mnew;
+        const int64_t n = kend - j0 < 256 ? kend - j0 : 256;
+#pragma unroll
+        for (int r = 0; r < NAIVE_COLS; ++r) {
+            const uint32_t d = t + 256 * r;
+            if (d >= HD) break;
+            float acc = o[r] * alpha;
+            for (int64_t jj = 0; jj < n; ++jj)
+                acc = fmaf(ps[jj], ld(p.v, p.kv_dtype, kvbase + (size_t)(j0 + jj) * HD + d), acc);
+            o[r] = acc;
+        }
+        __syncthreads();   // ps is rewritten by the next tile
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const size_t obase = (((size_t)b * p.tq + i) * p.hq + h) * HD;
+#pragma unroll
+    for (int r = 0; r < NAIVE_COLS; ++r) {
+        const uint32_t d = t + 256 * r;
+        if (d < HD) st(p.out, p.o_dtype, obase + d, o[r] * inv);
+    }
+}
+
+// fp32 K and V rounded to fp16 (round to nearest even) for the flash kernel,
+// n4 groups of 4 values each.
+__global__ __launch_bounds__(256) void attention_kv_f16_kernel(const float4v* k, const float4v* v, half4* ko,
+                                                               half4* vo, size_t n4)
+{
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n4; e += (size_t)gridDim.x * 256) {
+        ko[e] = __builtin_convertvector(k[e], half4);
+        vo[e] = __builtin_convertvector(v[e], half4);
+    }
+}
+
 // Split the key ranges only when the query tiles alone leave CUs idle, in the
 // shortest chunks whose work units still fit one round of workgroups (the
 // merge pass reads every unit's partial O back). At most 64 chunks per query
 // tile (the merge keeps their weights in LDS).
 void attention_plan(AttnParams& p, uint32_t cus)
 {
+    p.units = 0;
+    p.chunk_tiles = 0;
+    const uint32_t HD = p.head_dim;
+    const uint32_t qsz = p.q_dtype == DT_F32 ? 4 : 2;
+    // The flash kernel's operand rules (the reference's FA gate, attention.h:
+    // 916-945: Dh % 8 == 0, 16 <= Dh <= 256), plus 16-byte aligned operands
+    // and buffer ranges under 2^31 bytes; anything else takes the plain path.
+    const bool flash = HD % 8 == 0 && HD >= 16 && HD <= 256 && ((uintptr_t)p.q % 16) == 0 &&
+                       ((uintptr_t)p.k % 16) == 0 && ((uintptr_t)p.v % 16) == 0 &&
+                       (size_t)p.tkv * HD * 2 < (1ull << 31) && (size_t)p.tq * HD * qsz < (1ull << 31);
+    p.dp = !flash ? 0 : HD <= 64 ? 64 : HD <= 128 ? 128 : 256;
+    if (!p.dp) return;
     const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ, tiles = p.batch * p.hq * nqt;
     const uint32_t key_tiles = (p.tkv + fa::BKV - 1) / fa::BKV;
     const uint32_t min_chunk = std::max<uint32_t>(2, (key_tiles + 63) / 64);
-    p.units = 0;
     p.chunk_tiles = std::max<uint32_t>(min_chunk, key_tiles);
     if (tiles >= cus) return;
     for (uint32_t c = min_chunk; c <= key_tiles; ++c) {
@@ -673,26 +795,37 @@ void attention_plan(AttnParams& p, uint32_t cus)
     }
 }
 
-size_t attention_workspace_bytes(const AttnParams& p, uint32_t units)
+static size_t attention_kv_bytes(const AttnParams& p)
+{
+    if (!p.dp || p.kv_dtype != DT_F32) return 0;
+    const size_t n = (size_t)p.batch * p.hkv * p.tkv * p.head_dim;
+    return (2 * n * sizeof(half_t) + 255) & ~(size_t)255;
+}
+
+size_t attention_workspace_bytes(const AttnParams& p)
 {
     const size_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
-    return (size_t)p.batch * p.hq * units * fa::BQ * (p.head_dim + 2) * sizeof(float) +
-           (size_t)p.batch * p.hq * nqt * 2 * sizeof(uint32_t);
+    size_t bytes = attention_kv_bytes(p);
+    if (p.units)
+        bytes += (size_t)p.batch * p.hq * p.units * fa::BQ * (p.dp + 2) * sizeof(float) +
+                 (size_t)p.batch * p.hq * nqt * 2 * sizeof(uint32_t);
+    return bytes;
 }
 
 void attention_set_workspace(AttnParams& p, void* ws)
 {
-    p.ws_o = (float*)ws;
-    p.ws_ml = p.ws_o + (size_t)p.batch * p.hq * p.units * fa::BQ * p.head_dim;
+    const size_t kvb = attention_kv_bytes(p);
+    p.ws_kv = kvb ? ws : nullptr;
+    p.ws_o = (float*)((char*)ws + kvb);
+    p.ws_ml = p.ws_o + (size_t)p.batch * p.hq * p.units * fa::BQ * p.dp;
     p.ws_tab = (uint32_t*)(p.ws_ml + (size_t)p.batch * p.hq * p.units * fa::BQ * 2);
 }
 
 bool attention_ok(const AttnParams& p)
 {
-    return (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256) && p.hq > 0 && p.hkv > 0 &&
-           p.hq % p.hkv == 0 && ((uintptr_t)p.q % 16) == 0 && ((uintptr_t)p.k % 16) == 0 &&
-           ((uintptr_t)p.v % 16) == 0 && (size_t)p.tkv * p.head_dim * 2 < (1ull << 31) &&
-           (size_t)p.tq * p.head_dim * 2 < (1ull << 31);
+    const auto dt_ok = [](int d) { return d == DT_F32 || d == DT_F16; };
+    return p.hq > 0 && p.hkv > 0 && p.hq % p.hkv == 0 && p.head_dim > 0 && p.head_dim <= 256 * NAIVE_COLS &&
+           dt_ok(p.q_dtype) && dt_ok(p.kv_dtype) && dt_ok(p.o_dtype);
 }
 
 template <int D>
@@ -713,9 +846,29 @@ static hipError_t attention_launch_d(const AttnParams& p, hipStream_t s)
     return hipGetLastError();
 }
 
-hipError_t attention_launch(const AttnParams& p, hipStream_t s)
+hipError_t attention_launch(const AttnParams& p0, hipStream_t s)
 {
-    switch (p.head_dim) {
+    if (!p0.dp) {
+        hipLaunchKernelGGL(attention_naive_kernel, dim3(p0.tq, p0.hq, p0.batch), dim3(256), 0, s, p0);
+        return hipGetLastError();
+    }
+    AttnParams p = p0;
+    if (p.kv_dtype == DT_F32) {
+        if (!p.ws_kv) return hipErrorInvalidValue;
+        const size_t n = (size_t)p.batch * p.hkv * p.tkv * p.head_dim;
+        half_t* k16 = (half_t*)p.ws_kv;
+        half_t* v16 = k16 + n;
+        const size_t n4 = n / 4;
+        const uint32_t blocks = (uint32_t)std::min<size_t>((n4 + 255) / 256, 4096);
+        hipLaunchKernelGGL(attention_kv_f16_kernel, dim3(blocks), dim3(256), 0, s, (const float4v*)p.k,
+                           (const float4v*)p.v, (half4*)k16, (half4*)v16, n4);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        p.k = k16;
+        p.v = v16;
+        p.kv_dtype = DT_F16;
+    }
+    switch (p.dp) {
     case 64: return attention_launch_d<64>(p, s);
     case 128: return attention_launch_d<128>(p, s);
     case 256: return attention_launch_d<256>(p, s);

@@ -21,7 +21,13 @@ using namespace vai_dev;
 
 namespace {
 
-constexpr uint32_t kCUs = 256;
+// The current device's CU count for the plans; 256 (an MI355X) when no
+// device is visible, so that host-only plan queries see the target's plans.
+uint32_t plan_cus()
+{
+    int cus = 0;
+    return device_cus(&cus) == hipSuccess && cus > 0 ? (uint32_t)cus : 256u;
+}
 
 bool dtype_ok(int32_t d) { return d == VAI_DTYPE_F32 || d == VAI_DTYPE_F16; }
 size_t dtype_bytes(int32_t d) { return d == VAI_DTYPE_F16 ? 2 : 4; }
@@ -70,6 +76,39 @@ bool linear_packable(const vai_linear_args* a)
            a->K % 128 == 0 && (!a->gated || a->N % 2 == 0);
 }
 
+}   // namespace
+
+// ggmlSplitSize (/root/reference/vai/nodes/linear.h:600-604): the span each of
+// `splits` splits covers, rounded up to whole 256-blocks.
+uint32_t acc16_split_size(uint32_t K, uint32_t splits)
+{
+    return ((K + splits - 1) / splits + 255) / 256 * 256;
+}
+
+// The split count the reference gives an fp16-accumulating Linear with
+// splitSize 0 on the scalar tile path (otherLinearSplitCount -> ggmlGuessSplitCount,
+// linear.h:606-632, 2079-2084): the tile is ggml's scalar warptile of the
+// shape's tier (ggmlGuessTier / ggmlScalarWarptile, linear.h:485-546:
+// S = 32x32 when M or N <= 32, M = 64x64 when M or N <= 64, else L =
+// 128x128; wgM is the same for every subgroup size), split only a grid of at
+// most half (cores / tiles splits) or two thirds (3 splits) of the cores with
+// K >= 2048, at most 8, fewer while the last 256-rounded span would be empty.
+// `cores` is the device's compute-unit count, as computeBlockCount() reports.
+uint32_t acc16_guess_splits(uint32_t M, uint32_t N, uint32_t K, uint32_t cores)
+{
+    const uint32_t wg = (M <= 32 || N <= 32) ? 32 : (M <= 64 || N <= 64) ? 64 : 128;
+    if (cores == 0 || N < wg || M < wg || K < 2048) return 1;
+    const uint32_t tiles = ((M + wg - 1) / wg) * ((N + wg - 1) / wg);
+    uint32_t s = 1;
+    if (tiles <= cores / 2) s = cores / tiles;
+    else if (tiles <= cores * 2 / 3) s = 3;
+    s = std::min(s, 8u);
+    while (s > 1 && acc16_split_size(K, s) * (s - 1) >= K) --s;
+    return s;
+}
+
+namespace {
+
 LinearPlan plan_linear(const vai_linear_args* a)
 {
     LinearPlan p{};
@@ -87,9 +126,16 @@ LinearPlan plan_linear(const vai_linear_args* a)
         return p;
     }
     if (a->acc_dtype == VAI_DTYPE_F16 && !(a->i_dtype == VAI_DTYPE_F32 && a->w_dtype == VAI_DTYPE_F32)) {
-        // fp16 accumulation in the reference's order; split only on request
+        // fp16 accumulation in the reference's order. Each split starts its
+        // own fp16 chain, so the split count is the reference's: the
+        // requested span, else ggml's guess for its scalar tile.
         p.kind = LinearPlan::Acc16Tile;
-        p.split_size = a->split_size ? a->split_size : K;
+        if (a->split_size) {
+            p.split_size = a->split_size;
+        } else {
+            const uint32_t s = acc16_guess_splits(M, N, K, plan_cus());
+            p.split_size = s > 1 ? acc16_split_size(K, s) : K;
+        }
         p.splits = (K + p.split_size - 1) / p.split_size;
         p.workspace = p.splits > 1 ? (size_t)p.splits * M * N * 4 : 0;
         return p;
@@ -105,8 +151,8 @@ LinearPlan plan_linear(const vai_linear_args* a)
             // partial planes summed by the reduce pass.
             const uint32_t tiles = tiles_of(M, a->gated ? N / 2 : N, 256, a->gated ? 128 : 256);
             uint32_t splits = 1;
-            if (!a->gated && tiles < kCUs / 2) {
-                splits = std::max<uint32_t>(1, std::min<uint32_t>(kCUs / tiles, K / 256));
+            if (!a->gated && tiles < plan_cus() / 2) {
+                splits = std::max<uint32_t>(1, std::min<uint32_t>(plan_cus() / tiles, K / 256));
                 while (splits > 1 && K % (splits * 128) != 0) --splits;
             }
             g.splits = splits;
@@ -121,8 +167,8 @@ LinearPlan plan_linear(const vai_linear_args* a)
         }
         // fp32 problems with fewer 64x64 tiles than CUs: one launch over the
         // full K with a CU-filling tile count, instead of split-K + reduce
-        if (a->split_size == 0 && !a->gated && gemm_f32_ok(g) && tiles_of(M, N, 64, 64) < kCUs) {
-            const int nf = gemm_f32_nf(M, N, kCUs);
+        if (a->split_size == 0 && !a->gated && gemm_f32_ok(g) && tiles_of(M, N, 64, 64) < plan_cus()) {
+            const int nf = gemm_f32_nf(M, N, plan_cus());
             p.kind = LinearPlan::F32Small;
             p.bm = 32;
             p.bn = 16 * nf;
@@ -152,7 +198,7 @@ LinearPlan plan_linear(const vai_linear_args* a)
     Cand pick = cands[3];
     for (const Cand& c : cands) {
         if (f32 && c.bm == 256) continue;   // fp32 staging keeps 128-row tiles (LDS, registers)
-        if (tiles_of(M, ncols, c.bm, c.bn) >= kCUs) { pick = c; break; }
+        if (tiles_of(M, ncols, c.bm, c.bn) >= plan_cus()) { pick = c; break; }
     }
     p.tile = pick.t;
     p.bm = pick.bm;
@@ -163,15 +209,15 @@ LinearPlan plan_linear(const vai_linear_args* a)
         p.splits = (K + a->split_size - 1) / a->split_size;
     } else {
         uint32_t splits = 1;
-        if (f32 && tiles < kCUs && K >= 256) {
+        if (f32 && tiles < plan_cus() && K >= 256) {
             // fp32 matrix cores run at 1/16 of the fp16 rate, so a small fp32
             // GEMM is bound by how many SIMDs it keeps busy: aim at ~1.5
             // workgroups per CU (config 1, 96 tiles, K 768: 4 splits, 19 us,
             // against 36.7 us unsplit and 21 us with 3 or 6 splits)
-            splits = std::min<uint32_t>((3 * kCUs / 2 + tiles / 2) / tiles, K / 128);
+            splits = std::min<uint32_t>((3 * plan_cus() / 2 + tiles / 2) / tiles, K / 128);
             splits = std::max<uint32_t>(splits, 1);
-        } else if (tiles < kCUs / 2 && K >= 1024) {
-            splits = std::min<uint32_t>((kCUs + tiles - 1) / tiles, K / 256);
+        } else if (tiles < plan_cus() / 2 && K >= 1024) {
+            splits = std::min<uint32_t>((plan_cus() + tiles - 1) / tiles, K / 256);
             splits = std::max<uint32_t>(splits, 1);
         }
         p.split_size = splits > 1 ? ((K + splits - 1) / splits + bk - 1) / bk * bk : K;
@@ -396,11 +442,14 @@ static vai_status make_mask(MaskRule& m, uint32_t tq, uint32_t tkv, uint32_t cau
 static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
 {
     if (!a || !a->q || !a->k || !a->v) return VAI_ERR_INVALID_ARG;
-    if (a->i_dtype != VAI_DTYPE_F16 || !dtype_ok(a->o_dtype)) return VAI_ERR_DTYPE;
-    if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || a->tkv == 0 || a->hq % a->hkv != 0)
+    const auto f32_or_f16 = [](int32_t d) { return d == VAI_DTYPE_F32 || d == VAI_DTYPE_F16; };
+    if (!f32_or_f16(a->q_dtype) || !f32_or_f16(a->kv_dtype) || !dtype_ok(a->o_dtype)) return VAI_ERR_DTYPE;
+    if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || a->tkv == 0 || a->head_dim == 0 ||
+        a->hq % a->hkv != 0)
         return VAI_ERR_SHAPE;
     p = AttnParams{};
-    p.out = a->out; p.q = a->q; p.k = a->k; p.v = a->v; p.o_dtype = a->o_dtype;
+    p.out = a->out; p.q = a->q; p.k = a->k; p.v = a->v;
+    p.o_dtype = a->o_dtype; p.q_dtype = a->q_dtype; p.kv_dtype = a->kv_dtype;
     p.batch = a->batch; p.hq = a->hq; p.hkv = a->hkv; p.tq = a->tq; p.tkv = a->tkv; p.head_dim = a->head_dim;
     p.scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)a->head_dim);
     p.span = a->span;
@@ -409,15 +458,15 @@ static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
         return st;
     p.causal = p.mask.blocks == 1;
     if (!attention_ok(p)) return VAI_ERR_UNSUPPORTED;
-    attention_plan(p, kCUs);
+    attention_plan(p, plan_cus());
     return VAI_OK;
 }
 
 size_t vai_attention_workspace_size(const vai_attention_args* a)
 {
     AttnParams p;
-    if (attention_params(a, p) != VAI_OK || p.units == 0) return 0;
-    return attention_workspace_bytes(p, p.units);
+    if (attention_params(a, p) != VAI_OK) return 0;
+    return attention_workspace_bytes(p);
 }
 
 vai_status vai_attention_launch(const vai_attention_args* a, vai_stream_t stream)
@@ -426,8 +475,8 @@ vai_status vai_attention_launch(const vai_attention_args* a, vai_stream_t stream
     if (a && !a->out) return VAI_ERR_INVALID_ARG;
     vai_status st = attention_params(a, p);
     if (st != VAI_OK) return st;
-    if (p.units) {
-        const size_t need = attention_workspace_bytes(p, p.units);
+    const size_t need = attention_workspace_bytes(p);
+    if (need) {
         if (!a->workspace || a->workspace_bytes < need) return VAI_ERR_WORKSPACE;
         attention_set_workspace(p, a->workspace);
     }
@@ -523,7 +572,7 @@ vai_status vai_conv2d_launch(const vai_conv2d_args* a, vai_stream_t stream)
     g.residual = a->residual; g.residual_dtype = a->i_dtype;
     g.epilogue = a->epilogue; g.residual_order = a->residual_order; g.scalar_scale = 1.f;
     g.ci = a->ci; g.hi = a->hi; g.wi = a->wi; g.wo = wo; g.ks = a->kernel; g.stride = a->stride;
-    const GemmTile t = tiles_of(g.M, g.N, 128, 64) * a->batch >= kCUs ? GemmTile::T128x64 : GemmTile::T64x64;
+    const GemmTile t = tiles_of(g.M, g.N, 128, 64) * a->batch >= plan_cus() ? GemmTile::T128x64 : GemmTile::T64x64;
     return hip_status(gemm_launch(g, BKind::Im2col, EpiKind::Conv, t, (hipStream_t)stream));
 }
 
@@ -550,7 +599,7 @@ vai_status vai_attn_scores_launch(const vai_attn_scores_args* a, vai_stream_t st
         return st;
     g.causal = g.mask.blocks == 1;   // the diagonal fast path's flag (a block list takes the general one)
     if (scores_fast_ok(g)) return hip_status(scores_launch(g, (hipStream_t)stream));
-    const GemmTile t = tiles_of(g.M, g.N, 128, 128) * g.batch >= kCUs ? GemmTile::T128x128 : GemmTile::T64x64;
+    const GemmTile t = tiles_of(g.M, g.N, 128, 128) * g.batch >= plan_cus() ? GemmTile::T128x128 : GemmTile::T64x64;
     return hip_status(gemm_launch(g, BKind::Dense, EpiKind::Scores, t, (hipStream_t)stream));
 }
 

@@ -90,7 +90,10 @@ __global__ __launch_bounds__(256) void gemm_acc16_kernel(GemmParams p)
         __syncthreads();
     }
 
+    // clamp to +-65504 (linear-tile.comp:317-321); a NaN sum stays NaN (GLSL
+    // leaves clamp of a NaN undefined: keeping it makes the fault visible)
     const float lim = 65504.f;
+    const auto clamp16 = [lim](float x) { return x != x ? x : fminf(fmaxf(x, -lim), lim); };
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t row = m0 + ty + 16 * i;
@@ -99,9 +102,9 @@ __global__ __launch_bounds__(256) void gemm_acc16_kernel(GemmParams p)
         for (int j = 0; j < 4; ++j) {
             const uint32_t col = n0 + tx + 16 * j;
             if (col >= ncols) continue;
-            const float v = fminf(fmaxf((float)acc[0][i][j], -lim), lim);
+            const float v = clamp16((float)acc[0][i][j]);
             if constexpr (GATED) {
-                const float u = fminf(fmaxf((float)acc[G - 1][i][j], -lim), lim);
+                const float u = clamp16((float)acc[G - 1][i][j]);
                 if (p.splits > 1) {
                     float* P = (float*)p.C + (size_t)split * p.M * (2 * p.H);
                     P[(size_t)row * 2 * p.H + col] = v;

@@ -143,14 +143,21 @@ hipError_t gemm_f32_launch(const GemmParams& p, int nf, hipStream_t s);
 bool scores_fast_ok(const GemmParams& p);
 hipError_t scores_launch(const GemmParams& p, hipStream_t s);
 
-// Fused attention forward, fp16 Q/K/V [batch, heads, tokens, head_dim].
+// Fused attention forward. Q [batch, hq, tq, head_dim] in q_dtype, K / V
+// [batch, hkv, tkv, head_dim] in kv_dtype, O token-major [batch, tq, hq,
+// head_dim] in o_dtype (the layout of /root/reference/vai/shaders/
+// attention-fa.comp:8,96). Two paths: the MFMA flash kernel for head_dim % 8
+// == 0, 16 <= head_dim <= 256 (padded to dp = 64, 128 or 256 inside the
+// kernel; fp32 K / V are first rounded to fp16 copies in the workspace), and
+// a plain fp32 kernel for every other head dim (the reference's naive path).
 struct AttnParams {
-    void* out;                    // [batch, hq, tq, head_dim], o_dtype
+    void* out;                    // [batch, tq, hq, head_dim], o_dtype
     const void* q;
     const void* k;
     const void* v;
-    int o_dtype;
+    int o_dtype, q_dtype, kv_dtype;
     uint32_t batch, hq, hkv, tq, tkv, head_dim;
+    uint32_t dp;                  // flash kernel's padded head dim; 0: the naive kernel
     float scale;
     uint32_t causal, span;
     MaskRule mask;                // the same rule; blocks > 1 takes the general per-row bounds
@@ -160,17 +167,19 @@ struct AttnParams {
     // (max, sum) go to ws_o / ws_ml and a merge pass combines them, finding
     // each query tile's first unit and chunk count in ws_tab.
     uint32_t units, chunk_tiles;
-    float* ws_o;                  // [batch*hq*units][128][head_dim] (fp32, or fp16 O / l for fp16 output)
+    float* ws_o;                  // [batch*hq*units][128][dp] (fp32, or fp16 O / l for fp16 output)
     float* ws_ml;                 // [batch*hq*units][128][2]
     uint32_t* ws_tab;             // [batch*hq*query tiles][2]: first unit, chunks
+    void* ws_kv;                  // fp16 copies of fp32 K then V (flash path), else null
 };
 bool attention_ok(const AttnParams& p);
 // Units per head for p's shape (0 when no query tile needs splitting), and
 // the workspace the split needs.
 uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles);
-// Chooses the key split (chunk_tiles, units) for a GPU of `cus` compute units.
+// Chooses the path (dp) and the key split (chunk_tiles, units) for a GPU of
+// `cus` compute units.
 void attention_plan(AttnParams& p, uint32_t cus);
-size_t attention_workspace_bytes(const AttnParams& p, uint32_t units);
+size_t attention_workspace_bytes(const AttnParams& p);
 void attention_set_workspace(AttnParams& p, void* ws);
 hipError_t attention_launch(const AttnParams& p, hipStream_t s);
 

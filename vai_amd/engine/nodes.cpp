@@ -376,6 +376,7 @@ Attention::Attention(Config config) : config_(config)
     if (config_.numKVHeads == 0) config_.numKVHeads = config_.numQHeads;
     require(config_.numQHeads > 0 && config_.headDim > 0, "Attention: heads and headDim must be positive");
     require(config_.numQHeads % config_.numKVHeads == 0, "Attention: numQHeads must be a multiple of numKVHeads");
+    require(config_.kvCacheSize == 0 && !config_.kvCacheRing, "Attention: the KV cache is not supported");
     addSlot("out0", NodeSlot::output);
     addSlot("Q", NodeSlot::input);
     addSlot("K", NodeSlot::input);
@@ -387,16 +388,18 @@ vai_attention_args Attention::args(bool withBuffers) const
 {
     vai_attention_args a{};
     a.o_dtype = code(outputDtype());
-    a.i_dtype = code((*this)["Q"].dtype());
+    a.q_dtype = code((*this)["Q"].dtype());
+    a.kv_dtype = code((*this)["K"].dtype());
     a.batch = batch_;
     a.hq = config_.numQHeads;
     a.hkv = config_.numKVHeads;
     a.tq = tq_;
     a.tkv = tkv_;
     a.head_dim = config_.headDim;
-    a.scale = config_.scale;
-    apply_mask(a, config_.causal, config_.span, mask_);
-    // the size query needs non-null operands; their values do not matter
+    a.scale = 0.0f;   // 1/sqrt(headDim), attention.h:1254
+    apply_mask(a, false, 0, mask_);
+    // the size query needs non-null, 16-byte aligned operands (as the pool's
+    // buffers are); their values do not matter
     alignas(16) static char dummy[16];
     a.q = a.k = a.v = dummy;
     a.out = dummy;
@@ -423,13 +426,17 @@ void Attention::prepare()
     require(qs.back() == config_.headDim && ks.back() == config_.headDim, "Attention: headDim mismatch");
     require(qs[qs.size() - 3] == config_.numQHeads && ks[ks.size() - 3] == config_.numKVHeads,
             "Attention: head counts mismatch");
-    require(q.dtype() == Dtype::Fp16 && k.dtype() == Dtype::Fp16 && v.dtype() == Dtype::Fp16,
-            "Attention: Q, K and V must be fp16");
+    require(q.dtype() != Dtype::None && k.dtype() != Dtype::None, "Attention: Q, K, V need a dtype");
+    require(v.dtype() == k.dtype(), "Attention: K and V must share a dtype (attention.h:1014)");
     batch_ = outerSize(qs, 3);
     require(outerSize(ks, 3) == batch_, "Attention: Q and K batch axes differ");
     tq_ = qs[qs.size() - 2];
     tkv_ = ks[ks.size() - 2];
-    (*this)["out0"] = Tensor(qs, outputDtype());
+    // token-major [..., Tq, Hq, Dh] (attention.h:1220-1223): leading axes as they came
+    std::vector<uint32_t> os = qs;
+    os[os.size() - 3] = tq_;
+    os[os.size() - 2] = config_.numQHeads;
+    (*this)["out0"] = Tensor(os, outputDtype());
     const vai_attention_args a = args(false);
     const size_t ws = vai_attention_workspace_size(&a);
     (*this)["partialO"] = ws ? Tensor({uint32_t((ws + 3) / 4)}, Dtype::Fp32) : Tensor();

@@ -138,7 +138,7 @@ private:
 // of bits marks block k causal, span > 0 is a sliding window.
 using CausalBlockEnd = std::array<uint32_t, VAI_MAX_CAUSAL_BLOCKS - 1>;
 struct CausalMask {
-    uint32_t blockCount = 0;   // 0: the node's causal flag alone
+    uint32_t blockCount = 0;   // 0: none (AttentionScores: its causal flag; Attention: no mask)
     uint32_t bits = 0;
     CausalBlockEnd blockEnd{};
     uint32_t span = 0;
@@ -175,30 +175,35 @@ private:
 };
 
 // The reference's Attention node without a KV cache (/root/reference/vai/
-// nodes/attention.h:216-240, 979-1304): out0 = softmax(scale * Q K^T + mask) V
-// per head, Q [..., numQHeads, Tq, headDim], K / V [..., numKVHeads, Tkv,
-// headDim] fp16, out0 like Q in the node's output dtype. The mask is the
-// causal / sliding-window rule (the reference reads it from setCausalMask's
-// buffer). "partialO" holds the key-split partials when a launch uses them.
+// nodes/attention.h:77-129, 216-240, 979-1304): out0 = softmax(Q K^T /
+// sqrt(headDim) + mask) V per head. Q [..., numQHeads, Tq, headDim] fp32 or
+// fp16, K / V [..., numKVHeads, Tkv, headDim] in their own dtype (fp32 or
+// fp16), out0 token-major [..., Tq, numQHeads, headDim] in the node's output
+// dtype. Queries and keys align at their ends. No mask until setCausalMask
+// is called: every query attends every key. Any head dim. The KV cache
+// (kvCacheSize > 0) is not part of this build: the constructor rejects it.
+// "partialO" holds the workspace (fp16 K / V copies, key-split partials)
+// when a launch needs one.
 class Attention : public Node
 {
 public:
     struct Config {
         uint32_t headDim;
         uint32_t numQHeads;
-        uint32_t numKVHeads = 0;   // 0: numQHeads (no GQA)
-        bool causal = true;
-        uint32_t span = 0;         // sliding window; 0: none
-        float scale = 0.0f;        // 0: 1/sqrt(headDim), as attention.h:1254
+        uint32_t numKVHeads = 0;              // for GQA (Hkv < numQHeads); 0: numQHeads
+        uint32_t kvCacheSize = 0;             // must be 0 here: no cache
+        Dtype kvCacheDtype = Dtype::None;
+        bool kvCacheRing = false;
     } config_;
 
     explicit Attention(Config config);
     void prepare() override;
     void run(CommandStream& cmd) override;
     const char* kind() const override { return "Attention"; }
-    // The reference's setCausalMask role: replaces causal/span with the block
-    // mask. The reference rewrites a uniform buffer without re-recording; here
-    // the mask is part of the recorded launch, so the next forward re-records.
+    // The reference's setCausalMask role (a CausalMask made as
+    // writeCausalMask makes it; CausalMask::make(1) is plain causal). The
+    // reference rewrites a uniform buffer without re-recording; here the mask
+    // is part of the recorded launch, so the next forward re-records.
     void setCausalMask(const CausalMask& mask);
 
 private:

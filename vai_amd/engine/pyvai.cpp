@@ -208,14 +208,11 @@ PYBIND11_MODULE(_pyvai, m)
                  n.setCausalMask(node::CausalMask::make(bits, block_ends(ends), span));
              }, py::arg("bits"), py::arg("block_end") = std::vector<uint32_t>{}, py::arg("span") = 0);
     py::class_<node::Attention, Node>(nodes, "AttentionNode")
-        .def(py::init([](uint32_t num_q_heads, uint32_t head_dim, uint32_t num_kv_heads, bool causal, uint32_t span,
-                         float scale) {
-                 node::Attention::Config c{.headDim = head_dim, .numQHeads = num_q_heads, .numKVHeads = num_kv_heads,
-                                           .causal = causal, .span = span, .scale = scale};
+        .def(py::init([](uint32_t num_q_heads, uint32_t head_dim, uint32_t num_kv_heads) {
+                 node::Attention::Config c{.headDim = head_dim, .numQHeads = num_q_heads, .numKVHeads = num_kv_heads};
                  return std::make_unique<node::Attention>(c);
              }),
-             py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0, py::arg("causal") = true,
-             py::arg("span") = 0, py::arg("scale") = 0.0f)
+             py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0)
         .def("set_causal_mask", [](node::Attention& n, uint32_t bits, std::vector<uint32_t> ends, uint32_t span) {
                  n.setCausalMask(node::CausalMask::make(bits, block_ends(ends), span));
              }, py::arg("bits"), py::arg("block_end") = std::vector<uint32_t>{}, py::arg("span") = 0);

@@ -203,24 +203,23 @@ __host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt)
     return n <= 0 ? 1u : ((uint32_t)n + p.chunk_tiles - 1) / p.chunk_tiles;
 }
 
-// K / V tile copies of the 64 key rows from byte soff of the head into stage
-// t % 2: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
-// rows past Tkv and the padding past the head dim read as zero (buffer range
-// check).
+// K / V tile copies into stage t % 2, through resources that start at the
+// tile's first key row and end at the head's last: copy j of this wave fills
+// tile bytes [(wave*COPIES + j) KB, +1 KB); rows past Tkv and the padding past
+// the head dim read as zero (the range check, which sees the per-lane offset).
 template <int D>
 __device__ __forceinline__ void fa_issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, LDS_AS char* lds,
-                                         const uint32_t* coff, int soff, int t, int wave)
+                                         const uint32_t* coff, int t, int wave)
 {
     using L = fa::Lds<D>;
     LDS_AS char* st = lds + (t & 1) * L::STAGE + wave * L::COPIES * 1024;
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(st + j * 1024), 16, (int)coff[j], soff, 0,
-                                                 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(st + j * 1024), 16, (int)coff[j], 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(st + L::TILE + j * 1024), 16, (int)coff[j],
-                                                 soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (LDS_AS void*)(st + L::TILE + j * 1024), 16, (int)coff[j], 0, 0,
+                                                 0);
 }
 
 template <int N>
@@ -298,12 +297,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // lane l's 16 bytes land at physical chunk pc of row r and come from
     // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
     // (a chunk past the head dim points at byte 2^31, beyond any range)
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD), (short)0, (int)(Tkv * ROWG),
-        0x00020000);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD), (short)0, (int)(Tkv * ROWG),
-        0x00020000);
+    const char* kh0 = (const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD);
+    const char* vh0 = (const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD);
     uint32_t coff[L::COPIES];
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j) {
@@ -312,7 +307,12 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
     }
     const auto issue = [&](int t) __attribute__((always_inline)) {
-        fa_issue<D>(rk, rv, lds, coff, (int)((tb + t) * BKV * ROWG), t, wave);
+        const uint32_t row0 = (uint32_t)(tb + t) * BKV;   // < Tkv: a visible tile starts inside the keys
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(vh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
+        fa_issue<D>(rk, rv, lds, coff, t, wave);
     };
 
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units

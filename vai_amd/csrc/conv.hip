@@ -547,6 +547,267 @@ __global__ __launch_bounds__(CT * 16) __attribute__((amdgpu_waves_per_eu(4))) vo
     conv3_store<NF, CT>(p, red, epi_bs, co0, ho, b);
 }
 
+// ---- the pipelined form, for up to four 32-channel input blocks ----
+// The same LDS transpose and tap shift, but each wave owns 16 output
+// channels x the whole row over every input-channel block, so no partial sums
+// meet in LDS and the epilogue runs from the accumulators. A workgroup (4
+// waves, 64 output channels x one output row) issues everything it reads at
+// once, block by block -- the bias, then for each block j the wave's nine
+// weight fragments and its share of the block's input rows (CPW 1 KB copies,
+// the block padded to 4 KB per wave so that every wave issues the same
+// count) -- and starts on block j as soon as its own copies of j have landed
+// (a counted vmcnt: (NB - 1 - j) (9 + CPW) later operations may still be in
+// flight) and every wave has passed that point (s_barrier). Blocks occupy LDS
+// regions of their own, so no copy waits for a reader. The B fragments are
+// read by inline asm, which the compiler's wait insertion does not see (its
+// own ds_read_b64_tr_b16 would wait for every LDS copy in flight); a ring of
+// DPF steps is in flight ahead of the MFMAs, lgkmcnt counting the reads issued
+// since. The loop issues no scalar loads (they share lgkmcnt) and the block
+// boundaries are scheduling barriers, so the counts hold as written.
+// Measured at config 5 (MI355X, 100-launch graph): 6.75 us against 7.35 us for
+// the four-channel-block-waves form above. Variants that measured no better:
+// 8 waves splitting the blocks in two with an LDS sum (6.97), 32 output
+// channels per workgroup so that 320 of them cover every CU (7.09), the
+// epilogue through an LDS tile with 16-byte stores (7.46), deeper read rings
+// (DPF 5, 7: 7.06, 7.09), copy offsets computed once for all blocks (6.94).
+// What remains is serial per SIMD: 180 MFMAs (2880 cycles) per wave, about
+// 650 VALU instructions (copy offsets, the tap shift, the epilogue) and the
+// store of 3.3 MB.
+namespace cvp {
+template <int NF> struct Geo {
+    static constexpr uint32_t ROWB = 32 * NF;              // bytes per staged row (16 NF fp16 columns)
+    static constexpr uint32_t CHB = 3 * ROWB;              // bytes per channel (3 rows)
+    static constexpr uint32_t BLK = 32 * CHB;              // bytes of one 32-channel block
+    static constexpr uint32_t CPW = (BLK + 4095) / 4096;   // 1 KB copies per wave (4 waves) and block
+    static constexpr uint32_t CBB = CPW * 4096;            // LDS bytes per block
+};
+constexpr int DPF = 3;   // B steps in flight ahead of the MFMAs (6 reads)
+}
+
+template <int OFF>
+__device__ __forceinline__ half4 cv_tr16_asm(uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+    half4 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+__device__ __forceinline__ void cv_pin(half4& v) { asm volatile("" : "+v"(v)); }
+template <int N>
+__device__ __forceinline__ void cv_lgkm_wait()
+{
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+}
+template <int N>
+__device__ __forceinline__ void cv_vm_wait()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// The epilogue from the accumulators: lane (fr, fg) holds output channels
+// co_lane .. +3 at positions 16 f + fr; each store instruction writes 16
+// consecutive positions (64 bytes fp32) of four channels. Residual loads go
+// first (all in flight), then the values and the stores; RES and O16 are
+// template flags, so the straight-line code carries no per-element branches.
+// (Staging the tile through LDS for 16-byte stores measured slower: 7.5
+// against 6.4 us at config 5.)
+template <int EPI, bool RES, bool O16, int NF>
+__device__ __forceinline__ void conv3_pipe_store(const ConvParams& p, float4v (&acc)[NF], const float (&bias)[4],
+                                                 const float (&sc)[4], uint32_t co_lane, uint32_t ho, uint32_t b,
+                                                 int fr)
+{
+    const bool scaled = p.scale != nullptr, before = p.residual_order == 1;
+    const size_t HoWo = (size_t)p.ho * p.wo;
+    // channels of the lane's four that exist (a lane past Co stores nothing)
+    const uint32_t rows = co_lane < p.co ? min(p.co - co_lane, 4u) : 0u;
+    const size_t o0 = ((size_t)b * p.co + co_lane) * HoWo + (size_t)ho * p.wo + fr;
+    float rr[4][NF];
+    if constexpr (RES) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                // (a channel past Co reads the last one; its value is not stored)
+                const size_t o =
+                    ((size_t)b * p.co + min(co_lane + r, p.co - 1)) * HoWo + (size_t)ho * p.wo + fr + 16 * f;
+                rr[r][f] = p.residual_dtype == DT_F16 ? (float)((const half_t*)p.residual)[o]
+                                                      : ((const float*)p.residual)[o];
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        if ((uint32_t)r >= rows) break;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            float x = scaled ? fmaf(acc[f][r], sc[r], bias[r]) : acc[f][r] + bias[r];
+            if constexpr (RES) x += before ? rr[r][f] : 0.f;
+            x = cv_act<EPI>(x);
+            if constexpr (RES) x += before ? 0.f : rr[r][f];
+            const size_t o = o0 + (size_t)r * HoWo + 16 * f;
+            if constexpr (O16) ((half_t*)p.out)[o] = (half_t)x;
+            else ((float*)p.out)[o] = x;
+        }
+    }
+}
+
+template <int EPI, int NF>
+__device__ __forceinline__ void conv3_pipe_store_sel(const ConvParams& p, float4v (&acc)[NF], const float (&bias)[4],
+                                                     const float (&sc)[4], uint32_t co_lane, uint32_t ho, uint32_t b,
+                                                     int fr)
+{
+    const bool res = p.residual != nullptr, o16 = p.o_dtype == DT_F16;
+    if (res) {
+        if (o16) conv3_pipe_store<EPI, true, true>(p, acc, bias, sc, co_lane, ho, b, fr);
+        else conv3_pipe_store<EPI, true, false>(p, acc, bias, sc, co_lane, ho, b, fr);
+    } else {
+        if (o16) conv3_pipe_store<EPI, false, true>(p, acc, bias, sc, co_lane, ho, b, fr);
+        else conv3_pipe_store<EPI, false, false>(p, acc, bias, sc, co_lane, ho, b, fr);
+    }
+}
+
+template <int NF, int NB>
+__global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
+{
+    using G = cvp::Geo<NF>;
+    using cvp::DPF;
+    constexpr uint32_t ROWB = G::ROWB, CHB = G::CHB, CPW = G::CPW, CBB = G::CBB;
+    constexpr int S = 3 * NF;        // B steps per block: (kh, fragment)
+    constexpr int NW = 4;            // waves
+    extern __shared__ half8 smem[];
+    __attribute__((address_space(3))) char* xs = (__attribute__((address_space(3))) char*)(
+        __attribute__((address_space(3))) void*)smem;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = wave;   // output-channel group
+    const uint32_t co0 = blockIdx.x * 64, ho = blockIdx.y, b = blockIdx.z;
+    const int fr = lane & 15, fg = lane >> 4;
+    const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * 4 + g, CO16 - 1);   // past Co: discarded
+    const uint32_t co_lane = co0 + g * 16 + fg * 4;   // the lane's 4 output channels (accumulator rows)
+
+    // bias and scale of the lane's channels (a missing one reads the packed
+    // weight, at least Co values long, and is ignored)
+    float bias[4], sc[4];
+    {
+        const half_t* bsrc = p.bias ? (const half_t*)p.bias : p.wp;
+        const half_t* ssrc = p.scale ? (const half_t*)p.scale : p.wp;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t co = min(co_lane + r, p.co - 1);
+            const float bv = (float)bsrc[co];   // unconditional: no branch, no early wait
+            bias[r] = p.bias ? bv : 0.f;
+            sc[r] = (float)ssrc[co];
+        }
+    }
+
+    // Block j: this wave's weight fragments, then its share of the block's
+    // copies (9 + CPW operations).
+    const uint32_t plane_bytes = p.hi * ROWB;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const half_t*)p.x + (size_t)b * p.ci * p.hi * (16 * NF)), (short)0, (int)(p.ci * plane_bytes),
+        0x00020000);
+    half8 wa[NB][9];
+    static_for<NB>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = J;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+            wa[j][tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * NB + j) * 64 + lane) * 8);
+#pragma unroll
+        for (uint32_t k = 0; k < CPW; ++k) {
+            const uint32_t i0 = (k * NW + (uint32_t)wave) * 1024, pos = i0 + (uint32_t)lane * 16;
+            const uint32_t c = j * 32 + pos / CHB, w = pos % CHB, r = w / ROWB;
+            const int hi = (int)ho + (int)r - 1;
+            const uint32_t off = (pos < G::BLK && hi >= 0 && hi < (int)p.hi)
+                                     ? c * plane_bytes + (uint32_t)hi * ROWB + w % ROWB
+                                     : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(xs + j * CBB + i0),
+                                                     16, (int)off, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    });
+
+    float4v P[3][NF];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) P[k][f] = (float4v)0.f;
+    // B source lane (k, q) = (fr / 4, fr % 4) of group fg: channel 8 fg + k of
+    // the block, columns 4 q ..; the high half 4 channels on
+    const uint32_t lbase =
+        (uint32_t)reinterpret_cast<uintptr_t>(xs) + (8 * fg + (fr >> 2)) * CHB + (fr & 3) * 8;
+    static_for<NB>([&](auto J) __attribute__((always_inline)) {
+        constexpr int j = J;
+        cv_vm_wait<(NB - 1 - j) * (9 + CPW)>();   // this wave's copies of block j have landed
+        __builtin_amdgcn_s_barrier();               // ... and every other wave's
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t base = lbase + j * CBB;
+        half4 lo[S], hi[S];
+        auto rd = [&](auto SS) __attribute__((always_inline)) {
+            constexpr int s = SS, kh = s / NF, f = s % NF;
+            lo[s] = cv_tr16_asm<kh * ROWB + f * 32>(base);
+            hi[s] = cv_tr16_asm<4 * CHB + kh * ROWB + f * 32>(base);
+        };
+        static_for<DPF>([&](auto SS) __attribute__((always_inline)) { rd(SS); });
+        static_for<S>([&](auto SS) __attribute__((always_inline)) {
+            constexpr int s = SS, kh = s / NF, f = s % NF;
+            if constexpr (s + DPF < S) rd(std::integral_constant<int, s + DPF>{});
+            constexpr int later = (S - 1 - s) < DPF ? (S - 1 - s) : DPF;   // steps read after this one
+            cv_lgkm_wait<2 * later>();
+            cv_pin(lo[s]);
+            cv_pin(hi[s]);
+            const half8 bv = __builtin_shufflevector(lo[s], hi[s], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw)
+                P[kw][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[j][kh * 3 + kw], bv, P[kw][f], 0, 0, 0);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    });
+
+    // the taps combined: column x of fragment f is lane fr = x of each row
+    float4v acc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float a0 = cv_row_ror<1>(P[0][f][r]);
+            const float e0 = f > 0 ? cv_row_ror<1>(P[0][f > 0 ? f - 1 : 0][r]) : 0.f;
+            const float a2 = cv_row_ror<15>(P[2][f][r]);
+            const float e2 = f + 1 < NF ? cv_row_ror<15>(P[2][f + 1 < NF ? f + 1 : f][r]) : 0.f;
+            acc[f][r] = P[1][f][r] + (fr == 0 ? e0 : a0) + (fr == 15 ? e2 : a2);
+        }
+    switch (p.epilogue) {
+    case 1: conv3_pipe_store_sel<1, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    case 2: conv3_pipe_store_sel<2, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    case 3: conv3_pipe_store_sel<3, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    case 4: conv3_pipe_store_sel<4, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    case 5: conv3_pipe_store_sel<5, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    default: conv3_pipe_store_sel<0, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    }
+}
+
+template <int NF, int NB>
+static hipError_t launch_pipe(const ConvParams& p, hipStream_t s)
+{
+    constexpr uint32_t lds = NB * cvp::Geo<NF>::CBB;
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)conv3_pipe_kernel<NF, NB>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((conv3_pipe_kernel<NF, NB>), dim3((p.co + 63) / 64, p.ho, p.batch), dim3(256), lds, s, p);
+    return hipGetLastError();
+}
+
+template <int NF>
+static hipError_t launch_pipe_nb(const ConvParams& p, hipStream_t s)
+{
+    switch (cv::ci32(p.ci) / 32) {
+    case 1: return launch_pipe<NF, 1>(p, s);
+    case 2: return launch_pipe<NF, 2>(p, s);
+    case 3: return launch_pipe<NF, 3>(p, s);
+    default: return launch_pipe<NF, 4>(p, s);
+    }
+}
+
 // Whether the 3x3 LDS-transpose plan applies: fp16 NCHW rows of 16 NF
 // columns (NF <= 8), stride 1, aligned buffers, and the stage fits LDS.
 bool conv3_tr_ok(const ConvParams& p, int x_dt)
@@ -650,6 +911,18 @@ static hipError_t launch_ks(const ConvParams& p, int x_dt, size_t lds, hipStream
 
 hipError_t conv_launch(const ConvParams& p, int x_dt, hipStream_t s)
 {
+    if (conv3_tr_ok(p, x_dt) && cv::ci32(p.ci) <= 128) {
+        switch (p.wi / 16) {
+        case 1: return launch_pipe_nb<1>(p, s);
+        case 2: return launch_pipe_nb<2>(p, s);
+        case 3: return launch_pipe_nb<3>(p, s);
+        case 4: return launch_pipe_nb<4>(p, s);
+        case 5: return launch_pipe_nb<5>(p, s);
+        case 6: return launch_pipe_nb<6>(p, s);
+        case 7: return launch_pipe_nb<7>(p, s);
+        default: return launch_pipe_nb<8>(p, s);
+        }
+    }
     if (conv3_tr_ok(p, x_dt)) {
         switch (p.wi / 16) {
         case 1: return launch_tr<1>(p, s);

@@ -182,16 +182,19 @@ def build_cases(capi, stream, which):
                             2048 * 3072 * 2 + 16384 * 3072 * 2 + 2048 * 8192 * 2 * 2 + 3072 * 8192 * 2 + 2048 * 3072 * 2 * 2,
                             "f16", "ffn")
 
-    if "4" in which:   # attention scores; rotate S outputs past the MALL
-        q = D(f16(rng.standard_normal((8, 1024, 256))))
-        k = D(f16(rng.standard_normal((8, 1024, 256))))
-        outs = [capi.DeviceArray((8, 1024, 1024), np.float32) for _ in range(ROTATE_BYTES // (8 << 22) + 1)]
-        args = [capi.attn_scores_args(o, q, k, scale=1.0 / 16, causal=True) for o in outs]
+    if "4" in which:   # attention scores; rotate Q, K and S together past the MALL
+        n4 = ROTATE_BYTES // (8 << 22) + 1
+        q0 = f16(rng.standard_normal((8, 1024, 256)))
+        k0 = f16(rng.standard_normal((8, 1024, 256)))
+        qs = [D(q0) for _ in range(n4)]
+        ks = [D(k0) for _ in range(n4)]
+        outs = [capi.DeviceArray((8, 1024, 1024), np.float32) for _ in range(n4)]
+        args = [capi.attn_scores_args(o, q, k, scale=1.0 / 16, causal=True) for o, q, k in zip(outs, qs, ks)]
         refs = [ctypes.byref(a) for a in args]
 
         def fn4(i):
             capi.check(lib.vai_attn_scores_launch(refs[i % len(refs)], stream.ptr), "scores")
-        fn4.keep = [q, k, outs, args]
+        fn4.keep = [qs, ks, outs, args]
         cases["4"] = Case("attention scores Q,K[8,1024,256] fp16, S=QK^T/16 fp32 causal", "GB/s",
                           41943040 / 1e9, "hbm", HBM_PEAK_GBS, fn4, "scores_kernel<64, true> (64x64 tiles on and below the diagonal, each also storing its mirror tile's -inf; DMA staging, register epilogue)", 2 * 8 * 1024 * 1024 * 256,
                           41943040, "f16", "4")

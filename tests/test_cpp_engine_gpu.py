@@ -39,18 +39,6 @@ def test_gated_ffn_net_from_cpp(gpu, tmp_path, m, k, h, plan):
     assert_close(got, want, TRANS)
 
 
-@pytest.mark.gpu
-def test_mfma_rate_program(gpu):
-    """tests/cpp/mfma_rate measures the fp16 MFMA ceiling with constant and
-    with random operands (the roofline figures in the bench notes come from
-    it); here it runs briefly and must report six positive rates."""
-    exe = os.path.join(os.path.dirname(BIN), "mfma_rate")
-    r = subprocess.run([exe, "200"], capture_output=True, text=True, timeout=60)
-    assert r.returncode == 0, r.stderr
-    rates = [float(l.split(",")[1].split()[0]) for l in r.stdout.splitlines() if "TFLOP/s" in l]
-    assert len(rates) == 12 and all(v > 0 for v in rates), r.stdout
-
-
 BLOCK = os.path.join(os.path.dirname(BIN), "gated_ffn_block")
 
 

@@ -118,15 +118,27 @@ PROBE_SRC = os.path.join(HERE, "probe", "read_ceiling.hip")
 PROBE_LIB = os.path.join(HERE, "libvai_probe.so")
 
 
+MFMA_RATE_SRC = os.path.join(HERE, "probe", "mfma_rate.cpp")
+MFMA_RATE_BIN = os.path.join(HERE, "probe", "_bin", "mfma_rate")
+
+
 def _build_probe():
     """libvai_probe.so: bench.py's measurement kernels (the plain-read ceiling),
-    kept out of the product library."""
+    and the mfma_rate program (the matrix-core ceiling behind the roofline
+    notes), kept out of the product library."""
     tmp = PROBE_LIB + ".tmp"
     cmd = [HIPCC] + COMMON + DEVICE_FLAGS + ["-shared", PROBE_SRC, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("probe build failed:\n" + r.stderr)
     os.replace(tmp, PROBE_LIB)
+    os.makedirs(os.path.dirname(MFMA_RATE_BIN), exist_ok=True)
+    cmd = [HIPCC, "-x", "hip", "-O3", "-std=c++20", f"--offload-arch={ARCH}"] + DEVICE_FLAGS + [
+        MFMA_RATE_SRC, "-o", MFMA_RATE_BIN + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("mfma_rate build failed:\n" + r.stderr)
+    os.replace(MFMA_RATE_BIN + ".tmp", MFMA_RATE_BIN)
 
 
 def _build_cpp_programs():

@@ -279,7 +279,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     const uint32_t q0 = qt * BQ;
     const uint32_t hk = h / (p.hq / p.hkv);
     const uint32_t qsz = p.q_dtype == DT_F32 ? 4 : 2;
-    const char* Q = (const char*)p.q + ((size_t)b * p.hq + h) * Tq * HD * qsz;
+    const char* Q = uniform_ptr((const char*)p.q + ((size_t)b * p.hq + h) * Tq * HD * qsz);
 
     const uint32_t qrow = q0 + wave * QW + ql;
 
@@ -297,8 +297,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // lane l's 16 bytes land at physical chunk pc of row r and come from
     // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
     // (a chunk past the head dim points at byte 2^31, beyond any range)
-    const char* kh0 = (const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD);
-    const char* vh0 = (const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD);
+    const char* kh0 = uniform_ptr((const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD));
+    const char* vh0 = uniform_ptr((const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD));
     uint32_t coff[L::COPIES];
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j) {
@@ -307,7 +307,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
     }
     const auto issue = [&](int t) __attribute__((always_inline)) {
-        const uint32_t row0 = (uint32_t)(tb + t) * BKV;   // < Tkv: a visible tile starts inside the keys
+        // (< Tkv: a visible tile starts inside the keys)
+        const uint32_t row0 = __builtin_amdgcn_readfirstlane((uint32_t)(tb + t) * BKV);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(kh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -354,7 +355,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     half8 qf[KS];
     {
         const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(Q + (size_t)q0 * HD * qsz), (short)0, (int)((Tq - q0) * HD * qsz), 0x00020000);
+            (void*)uniform_ptr(Q + (size_t)q0 * HD * qsz), (short)0,
+            (int)__builtin_amdgcn_readfirstlane((Tq - q0) * HD * qsz), 0x00020000);
         const uint32_t qel = (wave * QW + ql) * HD + 8 * hf;   // first element of step 0
         if (p.q_dtype == DT_F32) {
 #pragma unroll

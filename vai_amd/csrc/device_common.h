@@ -44,6 +44,19 @@ __device__ __forceinline__ void st(void* p, int dt, size_t i, float v)
 // epilogue VALU-bound. tanh(y) = 1 - 2 / (e^{2y} + 1) saturates to +-1 for
 // large |y| (e^{2y} = inf gives 1 - 0) and keeps an absolute error of a few
 // ulp of 1 near 0.
+// A pointer every lane holds the same value of, moved to scalar registers:
+// a buffer resource built from it then stays scalar (a resource the compiler
+// cannot prove uniform is used through a readfirstlane loop around every
+// load).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p)
+{
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 

@@ -130,10 +130,10 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : (TRI ? 5 : 4)) void scores_kern
     }
 
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const half_t*)p.A + bz * p.a_batch_stride), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+        (void*)uniform_ptr((const half_t*)p.A + bz * p.a_batch_stride), (short)0, (int)((size_t)M * K * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const half_t*)p.B + (bz / p.b_group) * p.b_batch_stride), (short)0, (int)((size_t)N * K * 2),
-        0x00020000);
+        (void*)uniform_ptr((const half_t*)p.B + (bz / p.b_group) * p.b_batch_stride), (short)0,
+        (int)((size_t)N * K * 2), 0x00020000);
     // Copy i of wave w fills stage slots [(w*LOADS + i)*64, +64): Q rows first, then K rows.
     uint32_t off[LOADS];
     bool isk[LOADS];

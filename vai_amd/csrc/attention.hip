@@ -257,6 +257,10 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     uint32_t qt, chunk = 0;
     if (p.units == 0) {
         qt = nqt - 1 - unit;
+    } else if (unit < AttnParams::FA_UNIT_TAB) {
+        const uint32_t e = p.unit_tab[unit];   // (the host's walk below, done once per plan)
+        qt = e & 0xFFFFF;
+        chunk = e >> 20;
     } else {
         uint32_t u = unit;
         qt = nqt - 1;
@@ -792,6 +796,11 @@ void attention_plan(AttnParams& p, uint32_t cus)
         if ((uint64_t)u * p.batch * p.hq <= cus) {
             p.chunk_tiles = c;
             p.units = u;
+            // the kernel's unit -> (query tile, chunk) walk, from the last query tile
+            uint32_t n = 0;
+            for (uint32_t qt = nqt; qt-- > 0 && n < AttnParams::FA_UNIT_TAB;)
+                for (uint32_t ch = 0, nc = fa_chunks(p, qt); ch < nc && n < AttnParams::FA_UNIT_TAB; ++ch)
+                    p.unit_tab[n++] = qt | ch << 20;
             return;
         }
     }

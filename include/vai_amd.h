@@ -110,7 +110,7 @@ size_t vai_linear_workspace_size(const vai_linear_args* args);
  * No counterpart in the reference. Same arguments, kernels and results as
  * vai_linear_launch, but args->workspace is ignored: the split-K partials and
  * the M <= 8 gated intermediate go to a device array inside the library
- * (VAI_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until the
+ * (VAI_NOALLOC_SCRATCH_BYTES = 64 MiB per GPU, held from the library's load until the
  * process ends). Returns VAI_ERR_WORKSPACE when the launch needs more than that
  * (vai_linear_workspace_size() tells in advance). Nothing is allocated. All
  * calls on one GPU share its array: calls that overlap in time on that GPU

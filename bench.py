@@ -196,7 +196,7 @@ def build_cases(capi, stream, which):
             capi.check(lib.vai_attn_scores_launch(refs[i % len(refs)], stream.ptr), "scores")
         fn4.keep = [qs, ks, outs, args]
         cases["4"] = Case("attention scores Q,K[8,1024,256] fp16, S=QK^T/16 fp32 causal", "GB/s",
-                          41943040 / 1e9, "hbm", HBM_PEAK_GBS, fn4, "scores_kernel<64, true> (64x64 tiles on and below the diagonal, each also storing its mirror tile's -inf; DMA staging, register epilogue)", 2 * 8 * 1024 * 1024 * 256,
+                          41943040 / 1e9, "hbm", HBM_PEAK_GBS, fn4, "scores_strip_kernel<256> (64-row strips x 4 column classes, Q in registers, K tiles by DMA, hidden tiles stored as -inf, register epilogue)", 2 * 8 * 1024 * 1024 * 256,
                           41943040, "f16", "4")
 
     if "attn" in which:   # the whole attention at config 4's shape: scores, softmax and P.V fused

@@ -215,10 +215,15 @@ def run_scores(capi, q, k, **kw):
     (3, 3, 257, 257, 128, True, 0, np.float16),
     (12, 4, 130, 130, 64, True, 0, np.float16),      # 12 heads: a partial second round over the 8 XCDs
     (17, 17, 64, 96, 64, False, 0, np.float16),
-    # square causal, Tq a multiple of 64: only the tiles on and below the
-    # diagonal are launched, each writing its mirror tile's -inf
+    # square causal, Tq a multiple of 64, head dim 64/128/256: the strip form
+    # (64-row strips, four column classes, Q held in registers)
     (8, 2, 512, 512, 128, True, 0, np.float16),      # 8 heads (one per XCD), GQA
-    (3, 3, 320, 320, 64, True, 0, np.float16),       # heads not a multiple of 8
+    (3, 3, 320, 320, 64, True, 0, np.float16),       # heads not a multiple of 8, 5 strips
+    (8, 8, 1024, 1024, 256, True, 0, np.float16),    # config 4's shape
+    (2, 1, 128, 128, 256, True, 0, np.float16),      # 2 strips: classes with no computed tile
+    # other head dims: only the tiles on and below the diagonal are launched,
+    # each writing its mirror tile's -inf
+    (2, 2, 192, 192, 192, True, 0, np.float16),
 ])
 def test_scores(gpu, hq, hkv, tq, tkv, d, causal, span, dt):
     rng = np.random.default_rng(0)

@@ -8,9 +8,11 @@
 //    each head's tiles on one XCD when the heads come in multiples of 8;
 //    tiles the mask hides entirely are written as -inf and never touch Q, K
 //    or the matrix cores; under a plain causal mask over a square S (a
-//    multiple of 64) only the tiles on and below the diagonal are launched,
-//    and each writes its mirror tile's -inf while its Q/K stages load
-//    (config 4: 10.7-11.0 against 11.4-11.6 us with every tile launched);
+//    multiple of 64) with head dim 64, 128 or 256, the strip form below
+//    takes over; for other head dims only the tiles on and below the
+//    diagonal are launched, and each writes its mirror tile's -inf while its
+//    Q/K stages load (config 4 with Q and K resident, before the strip
+//    form: 10.7-11.0 us against 11.4-11.6 with every tile launched);
 //  * Q and K rows are copied global->LDS (buffer_load ... lds) in 64-wide
 //    head-dim stages, double buffered; 4 waves x (T/2 x T/2 of 32x32x16
 //    MFMAs); 64 KB (32 KB) of LDS, so two (four) workgroups share a CU and
@@ -259,6 +261,146 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : (TRI ? 5 : 4)) void scores_kern
     });
 }
 
+// ---- strip form: plain causal scores over a square S (head dim 64-256) ----
+// Workgroup (head, 64-row strip s, column class par of 4) owns the strip's
+// 64x64 tiles j = par, par + 4, ..: those right of the diagonal (j > s) are
+// hidden and only stored as -inf (first, while the operands load); the
+// others are computed. Each wave keeps its 32 query rows of the strip in
+// registers for the whole walk (the MFMA A operand, loaded once), so Q is
+// read once per strip and class instead of once per tile, and the K tiles
+// stream through two LDS slots by buffer_load ... lds (16-byte chunks
+// XOR-swizzled by row), the next tile in flight while this one runs. Every
+// workgroup stores the same n / 4 tiles whatever its share of the computed
+// ones, and at most n / 4 are computed. Config 4 (512 workgroups, two per CU):
+// 10.8-10.9 us against 11.2-11.3 for the 64x64-tile grid in the same runs;
+// two classes (256 workgroups, up to 8 computed tiles each) 13.4, eight
+// (1024, two rounds at two per CU) 14.6, the classes of a CU's two units
+// balanced by reversing the second half of the units 11.1-11.2, stores
+// without the non-temporal hint 15.7.
+template <int D>
+__global__ __launch_bounds__(256, 2) void scores_strip_kernel(GemmParams p)
+{
+    constexpr int T = 64, ROWB = D * 2, CHR = D / 8, KS = D / 16;
+    constexpr int TILE = T * ROWB, COPIES = TILE / 4096;   // 1 KB copies per wave per tile
+    constexpr int SWZ = CHR >= 16 ? 15 : 7;                 // chunk bits XORed with the row
+    extern __shared__ half8 lds[];
+    LDS_AS char* lds_base = (LDS_AS char*)(LDS_AS void*)lds;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1, fr = lane & 31, fk = lane >> 5;
+    const uint32_t n = p.M / T, N = p.N;   // strips (= tiles per row); S row length
+    // workgroup -> (head, unit); a head's units on one XCD when heads come in 8s
+    uint32_t bz = blockIdx.z, u = blockIdx.x;
+    if (gridDim.z % 8 == 0) {
+        const uint32_t nt = gridDim.x, w = blockIdx.x + nt * blockIdx.z;
+        const uint32_t g = w / (8 * nt), r = w % (8 * nt);
+        bz = g * 8 + r % 8;
+        u = r / 8;
+    }
+    constexpr uint32_t NC = 4;                          // column classes: tiles j = par, par + NC, ..
+    const uint32_t s = n - 1 - u / NC, par = u % NC;
+    const uint32_t m0 = s * T;
+    float* S = (float*)p.C + bz * p.c_batch_stride;
+    const half_t* Qh = (const half_t*)p.A + bz * p.a_batch_stride;
+    const half_t* Kh = uniform_ptr((const half_t*)p.B + (bz / p.b_group) * p.b_batch_stride);
+
+    // hidden tiles: the wave's 32x32 quadrant, 16 bytes per lane, 8 rows per store
+    {
+        const float4v ninf = (float4v)(-__builtin_inff());
+        const uint32_t r0 = m0 + wm * 32, c = wn * 32 + (lane % 8) * 4;
+        for (uint32_t j = par + ((s + NC - par) / NC) * NC; j < n; j += NC)
+#pragma unroll
+            for (int it = 0; it < 4; ++it)
+                __builtin_nontemporal_store(ninf, (float4v*)(S + (size_t)(r0 + it * 8 + lane / 8) * N + j * T + c));
+    }
+    const uint32_t nc = s >= par ? (s - par) / NC + 1 : 0;   // computed tiles
+    if (nc == 0) return;
+
+    // K tile copies: copy i of wave w fills tile bytes [(w*COPIES + i) KB, +1 KB);
+    // lane l's 16 bytes land at physical chunk pc of row r, from logical chunk pc ^ (r & SWZ)
+    uint32_t coff[COPIES];
+#pragma unroll
+    for (int i = 0; i < COPIES; ++i) {
+        const int byte = (wave * COPIES + i) * 1024 + lane * 16, r = byte / ROWB, pc = (byte % ROWB) / 16;
+        coff[i] = (uint32_t)(r * ROWB + (pc ^ (r & SWZ)) * 16);
+    }
+    auto issue = [&](uint32_t c) __attribute__((always_inline)) {
+        const uint32_t key0 = __builtin_amdgcn_readfirstlane((par + NC * c) * T);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(Kh + (size_t)key0 * D), (short)0, TILE, 0x00020000);
+        LDS_AS char* dst = lds_base + (c & 1) * TILE + wave * COPIES * 1024;
+#pragma unroll
+        for (int i = 0; i < COPIES; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LDS_AS void*)(dst + i * 1024), 16, (int)coff[i], 0, 0, 0);
+    };
+
+    // the wave's query rows m0 + 32 wm + fr, dims 16 ks + 8 fk (the A operand)
+    half8 qf[KS];
+    {
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform_ptr(Qh + (size_t)(m0 + wm * 32) * D), (short)0, 32 * ROWB, 0x00020000);
+        const uint32_t qoff = (uint32_t)(fr * D + 8 * fk) * 2;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            qf[ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(qoff + 32 * ks), 0, 0));
+    }
+    issue(0);
+    if (nc > 1) issue(1);
+
+    // B fragments: key row wn*32 + fr of the tile, logical chunk 2 ks + fk
+    const int brow = wn * 32 + fr;
+    const float scale = p.scalar_scale;
+    const uint32_t rw0 = wm * 32 + 4 * fk, cw0 = wn * 32 + fr;   // the lane's row / column in a tile
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)uniform_ptr(S + (size_t)m0 * N), (short)0, 0x7FFFFFFF, 0x00020000);
+    for (uint32_t c = 0; c < nc; ++c) {
+        // tile c landed in every wave's share (tile c + 1's copies may be in flight)
+        if (c + 1 < nc) sc_wait_vmcnt<COPIES>();
+        else sc_wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        const LDS_AS char* kt = lds_base + (c & 1) * TILE + brow * ROWB;
+        // all of the tile's B fragments read first, then the MFMAs (read one
+        // at a time, each MFMA waited out its read's latency)
+        half8 bf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) bf[ks] = *(const LDS_AS half8*)(kt + (((2 * ks + fk) ^ (brow & SWZ)) * 16));
+        float16v acc = (float16v)0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qf[ks], bf[ks], acc, 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);   // the reads, in order, ...
+        __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);   // ... then the MFMAs
+        const uint32_t j = par + NC * c;
+        if (c + 2 < nc) {
+            // every wave is done reading this slot before it is refilled
+            __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+            __builtin_amdgcn_s_barrier();
+            issue(c + 2);
+        }
+        // D[i][j] of the 32x32 fragment: lane j + 32 ((i/4) % 2), register
+        // (i % 4) + 4 (i / 8); the diagonal tile hides column > row
+        const bool diag = j == s;
+        const uint32_t lane_off = (rw0 * N + j * T + cw0) * 4;
+        static_for<16>([&](auto R) __attribute__((always_inline)) {
+            constexpr int r = R, rc = (r % 4) + 8 * (r / 4);
+            float v = acc[r] * scale;
+            if (diag) v = (int)cw0 > (int)rw0 + rc ? -__builtin_inff() : v;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), out,
+                                                  (int)(lane_off + (uint32_t)rc * N * 4), 0, kNonTemporal);
+        });
+    }
+}
+
+template <int D>
+static hipError_t scores_launch_strip(const GemmParams& p, hipStream_t s)
+{
+    constexpr int LDS = 2 * 64 * D * 2;
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)scores_strip_kernel<D>, LDS);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(scores_strip_kernel<D>, dim3(4 * (p.M / 64), 1, p.batch), dim3(256), LDS, s, p);
+    return hipGetLastError();
+}
+
 bool scores_fast_ok(const GemmParams& p)
 {
     return p.a_dtype == DT_F16 && p.b_dtype == DT_F16 && p.K % 64 == 0 &&
@@ -295,8 +437,12 @@ static hipError_t scores_launch_tri(const GemmParams& p, hipStream_t s)
 hipError_t scores_launch(const GemmParams& p, hipStream_t s)
 {
     if (p.causal && p.mask.blocks == 1 && p.mask.bits == 1 && p.span == 0 && p.mask.span == 0 && p.M == p.N &&
-        p.causal_offset == 0 && p.M % 64 == 0)
+        p.causal_offset == 0 && p.M % 64 == 0) {
+        if (p.K == 256) return scores_launch_strip<256>(p, s);
+        if (p.K == 128) return scores_launch_strip<128>(p, s);
+        if (p.K == 64) return scores_launch_strip<64>(p, s);
         return scores_launch_tri(p, s);
+    }
     return (p.causal || p.span || p.mask.blocks > 1) ? scores_launch_t<64>(p, s) : scores_launch_t<128>(p, s);
 }
 

@@ -287,66 +287,6 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 
     const uint32_t qrow = q0 + wave * QW + ql;
 
-    // visible key tiles of the query tile, then this unit's chunk of them
-    int64_t tb, te;
-    fa_tile_range(p, qt, tb, te);
-    if (p.units != 0) {
-        const int64_t c0 = tb + (int64_t)chunk * p.chunk_tiles;
-        te = std::min<int64_t>(te, c0 + p.chunk_tiles);
-        tb = c0;
-    }
-    const int ntiles = (int)__builtin_amdgcn_readfirstlane((int)std::max<int64_t>(te - tb, 0));
-
-    // K / V tile copies: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
-    // lane l's 16 bytes land at physical chunk pc of row r and come from
-    // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
-    // (a chunk past the head dim points at byte 2^31, beyond any range)
-    const char* kh0 = uniform_ptr((const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD));
-    const char* vh0 = uniform_ptr((const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD));
-    uint32_t coff[L::COPIES];
-#pragma unroll
-    for (int j = 0; j < L::COPIES; ++j) {
-        const int byte = (wave * L::COPIES + j) * 1024 + lane * 16;
-        const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16, lc = swz<D>(r, pc);
-        coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
-    }
-    const auto issue = [&](int t) __attribute__((always_inline)) {
-        // (< Tkv: a visible tile starts inside the keys)
-        const uint32_t row0 = __builtin_amdgcn_readfirstlane((uint32_t)(tb + t) * BKV);
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(kh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(vh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
-        fa_issue<D>(rk, rv, lds, coff, t, wave);
-    };
-
-    const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
-    const uint32_t qclip = qrow < Tq ? qrow : Tq - 1;
-    const int64_t row_kend = p.mask.key_end(qclip), row_kbeg = p.mask.key_start(qclip);
-    float m = -__builtin_inff(), l = 0.f;
-    float16v o[DF];
-#pragma unroll
-    for (int d = 0; d < DF; ++d) o[d] = (float16v)0.f;
-
-    // V^T fragment reads: in each 16-lane group g the transposed read gives
-    // lane j head-dim value dg + j and 4 consecutive keys; source lane s of
-    // the group points at key (base + s / 4), values dg + 4 (s % 4) .. +3.
-    const int g = lane >> 4, s16 = lane & 15;
-    const int vrow = s16 >> 2, vcol = 16 * (g & 1) + 4 * (s16 & 3);   // + 32 d; key + 16 kk + 8 part
-    const int vkey = 4 * (g >> 1);
-    // lane parts of the fragment addresses (fa_kfrag, fa_vfrag), stage 0
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
-    constexpr int NK = fa_nk<D>;
-    uint32_t kofs[NK], vofs[2];
-#pragma unroll
-    for (int j = 0; j < NK; ++j)
-        kofs[j] = lds0 + ql * L::ROWB +
-                  (((2 * (j & 3) + hf) ^ swz_f(ql & 7)) + (D >= 128 ? (8 * (j >> 2)) ^ (ql & 8) : 0)) * 16;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-        vofs[j] = lds0 + (vkey + vrow) * L::ROWB + ((4 * j + (vcol >> 3)) ^ swz_f((vkey + vrow) & 7)) * 16 +
-                  (vcol & 7) * 2;
-
     // The wave's 32 query rows go straight into VGPRs as the B operand of
     // S^T = K Q^T (lane l: query l % 32, head-dim values 16 s + 8 (l / 32)
     // .. +7 of step s; rows past Tq read as zero through the resource's
@@ -380,13 +320,73 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
             }
         }
     }
-    if (ntiles > 0) issue(0);
-    if (ntiles > 1) {
-        issue(1);
-        fa_wait_vmcnt<2 * L::COPIES>();
-    } else {
-        fa_wait_vmcnt<0>();
+
+    // visible key tiles of the query tile, then this unit's chunk of them
+    int64_t tb, te;
+    fa_tile_range(p, qt, tb, te);
+    if (p.units != 0) {
+        const int64_t c0 = tb + (int64_t)chunk * p.chunk_tiles;
+        te = std::min<int64_t>(te, c0 + p.chunk_tiles);
+        tb = c0;
     }
+    const int ntiles = (int)__builtin_amdgcn_readfirstlane((int)std::max<int64_t>(te - tb, 0));
+
+    // K / V tile copies: copy j of this wave fills tile bytes [(wave*COPIES + j) KB, +1 KB);
+    // lane l's 16 bytes land at physical chunk pc of row r and come from
+    // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
+    // (a chunk past the head dim points at byte 2^31, beyond any range)
+    const char* kh0 = uniform_ptr((const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD));
+    const char* vh0 = uniform_ptr((const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD));
+    uint32_t coff[L::COPIES];
+#pragma unroll
+    for (int j = 0; j < L::COPIES; ++j) {
+        const int byte = (wave * L::COPIES + j) * 1024 + lane * 16;
+        const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16, lc = swz<D>(r, pc);
+        coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
+    }
+    const auto issue = [&](int t) __attribute__((always_inline)) {
+        // (< Tkv: a visible tile starts inside the keys)
+        const uint32_t row0 = __builtin_amdgcn_readfirstlane((uint32_t)(tb + t) * BKV);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(vh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
+        fa_issue<D>(rk, rv, lds, coff, t, wave);
+    };
+
+    if (ntiles > 0) issue(0);
+    if (ntiles > 1) issue(1);
+
+    // (the rest of the set-up runs while Q and the first tiles load)
+    const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
+    const uint32_t qclip = qrow < Tq ? qrow : Tq - 1;
+    const int64_t row_kend = p.mask.key_end(qclip), row_kbeg = p.mask.key_start(qclip);
+    float m = -__builtin_inff(), l = 0.f;
+    float16v o[DF];
+#pragma unroll
+    for (int d = 0; d < DF; ++d) o[d] = (float16v)0.f;
+
+    // V^T fragment reads: in each 16-lane group g the transposed read gives
+    // lane j head-dim value dg + j and 4 consecutive keys; source lane s of
+    // the group points at key (base + s / 4), values dg + 4 (s % 4) .. +3.
+    const int g = lane >> 4, s16 = lane & 15;
+    const int vrow = s16 >> 2, vcol = 16 * (g & 1) + 4 * (s16 & 3);   // + 32 d; key + 16 kk + 8 part
+    const int vkey = 4 * (g >> 1);
+    // lane parts of the fragment addresses (fa_kfrag, fa_vfrag), stage 0
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+    constexpr int NK = fa_nk<D>;
+    uint32_t kofs[NK], vofs[2];
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+        kofs[j] = lds0 + ql * L::ROWB +
+                  (((2 * (j & 3) + hf) ^ swz_f(ql & 7)) + (D >= 128 ? (8 * (j >> 2)) ^ (ql & 8) : 0)) * 16;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        vofs[j] = lds0 + (vkey + vrow) * L::ROWB + ((4 * j + (vcol >> 3)) ^ swz_f((vkey + vrow) & 7)) * 16 +
+                  (vcol & 7) * 2;
+
+    if (ntiles > 1) fa_wait_vmcnt<2 * L::COPIES>();
+    else fa_wait_vmcnt<0>();
     for (int t = 0; t < ntiles; ++t) {
         // tile t landed in every wave's share (tile t + 1's copies may be in flight)
         if (t > 0) {
@@ -570,21 +570,39 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         wml[0] = m;
         wml[1] = l;
     }
-    // Partials keep the padded rows (D wide); the output is token-major
-    // [batch, Tq, Hq, HD]: query row r of head h at row (b Tq + r) Hq + h.
+    // Partials keep the padded rows (D wide, the wave's 32 rows contiguous);
+    // the output is token-major [batch, Tq, Hq, HD]: query row r of head h at
+    // row (b Tq + r) Hq + h. One loop per destination, so that no branch sits
+    // between the LDS reads and the stores.
     const uint32_t wrow0 = q0 + wave * QW;   // the wave's first query row
+    constexpr int NJ = QW * CR / 64;         // 16-byte chunks per lane
+    if (part16) {
+        half_t* dst = uniform_ptr((half_t*)p.ws_o + (gid * BQ + wave * QW) * D);
 #pragma unroll
-    for (int j = 0; j < QW * CR / 64; ++j) {
-        const int e = j * 64 + lane, r = e / CR, c = e % CR;
-        const float4v v = ob[r * CR + (c ^ (r & 15))];
-        if (partial) {
-            const size_t o0 = (gid * BQ + wave * QW + r) * D + 4 * c;
-            if (part16) *(half4*)((half_t*)p.ws_o + o0) = __builtin_convertvector(v, half4);
-            else *(float4v*)(p.ws_o + o0) = v;
-        } else if (wrow0 + r < Tq && 4u * c < HD) {
-            const size_t o0 = (((size_t)b * Tq + wrow0 + r) * p.hq + h) * HD + 4 * c;
-            if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o0) = __builtin_convertvector(v, half4);
-            else *(float4v*)((float*)p.out + o0) = v;
+        for (int j = 0; j < NJ; ++j) {
+            const int e = j * 64 + lane, r = e / CR, c = e % CR;
+            *(half4*)(dst + r * D + 4 * c) = __builtin_convertvector(ob[r * CR + (c ^ (r & 15))], half4);
+        }
+    } else if (partial) {
+        float* dst = uniform_ptr(p.ws_o + (gid * BQ + wave * QW) * D);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int e = j * 64 + lane, r = e / CR, c = e % CR;
+            *(float4v*)(dst + r * D + 4 * c) = ob[r * CR + (c ^ (r & 15))];
+        }
+    } else {
+        const bool o16 = p.o_dtype == DT_F16;
+        const size_t rstride = (size_t)p.hq * HD;   // elements from one query row to the next
+        const size_t base = (((size_t)b * Tq + wrow0) * p.hq + h) * HD;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int e = j * 64 + lane, r = e / CR, c = e % CR;
+            const float4v v = ob[r * CR + (c ^ (r & 15))];
+            if (wrow0 + r < Tq && 4u * c < HD) {
+                const size_t o0 = base + r * rstride + 4 * c;
+                if (o16) *(half4*)((half_t*)p.out + o0) = __builtin_convertvector(v, half4);
+                else *(float4v*)((float*)p.out + o0) = v;
+            }
         }
     }
 }

@@ -258,7 +258,9 @@ def build_cases(capi, stream, which):
         flops = 2 * ho * ho * co * ci * ks * ks
         byts = ci * hw * hw * 2 + co * ci * ks * ks * 2 + co * 2 + co * ho * ho * 4
         cases[key] = Case(f"YOLOX-s {ks}x{ks}/s{st} conv in[1,{ci},{hw},{hw}] W[{co},{ci},{ks},{ks}] fp16 +bias SiLU, fp32 out",
-                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnc, f"conv_kernel<{ks}> (implicit GEMM, packed weight)",
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnc,
+                          "conv1_pipe_kernel<8> (pointwise: 16 flat positions x 64 output channels per workgroup)" if ks == 1
+                          else f"conv_kernel<{ks}> (implicit GEMM, packed weight)",
                           flops, byts, "f16", key)
     if "read" in which or "empty" in which or "write" in which:
         # the ceiling for config 2: a plain read of W's 32 MiB, rotated like the

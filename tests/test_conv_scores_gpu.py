@@ -157,6 +157,26 @@ def test_conv3_lds_transpose_scale_residual(gpu, order):
     assert_close(got, want, FP16)
 
 
+@pytest.mark.parametrize("ci, co, h, w, batch, order, odt, rdt", [
+    (40, 48, 6, 4, 2, 0, np.float16, np.float16),      # channel and output-channel tails, 24 positions (half a fragment)
+    (256, 128, 8, 10, 1, 1, np.float32, np.float32),   # eight channel blocks, residual before the activation
+    (32, 200, 4, 2, 3, 0, np.float32, np.float16),     # a single partial fragment per image, batch 3
+])
+def test_conv1_pointwise(gpu, ci, co, h, w, batch, order, odt, rdt):
+    """The pointwise kernel (1x1, stride 1, fp16 input: positions taken as one
+    flat row of 16-wide fragments) with scale, residual and output dtypes."""
+    rng = np.random.default_rng(ci + co)
+    wt = draw(normal((co, ci, 1, 1), 1.0 / np.sqrt(ci)), rng, np.float16)
+    b = draw((co,), rng, np.float16)
+    s = draw(uniform((co,), 0.5, 1.5), rng, np.float16)
+    x = draw((batch, ci, h, w), rng, np.float16)
+    r = draw((batch, co, h, w), rng, rdt)
+    print(f"conv1 ci={ci} co={co} h={h} w={w} batch={batch}", flush=True)
+    got = run_conv(gpu, x, wt, b, s, r, out_dtype=odt, epi="SILU", order=order).astype(np.float32)
+    want = oracle.conv2d(x, wt, b, s, r, epi="SILU", order=order)
+    assert_close(got, want, FP16)
+
+
 class _Offset:
     """A buffer `off` bytes into a larger DeviceArray (to miss an alignment on purpose)."""
 

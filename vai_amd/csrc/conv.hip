@@ -551,28 +551,36 @@ __global__ __launch_bounds__(CT * 16) __attribute__((amdgpu_waves_per_eu(4))) vo
 // The same LDS transpose and tap shift, but each wave owns 16 output
 // channels x the whole row over every input-channel block, so no partial sums
 // meet in LDS and the epilogue runs from the accumulators. A workgroup (4
-// waves, 64 output channels x one output row) issues everything it reads at
-// once, block by block -- the bias, then for each block j the wave's nine
-// weight fragments and its share of the block's input rows (CPW 1 KB copies,
-// the block padded to 4 KB per wave so that every wave issues the same
-// count) -- and starts on block j as soon as its own copies of j have landed
-// (a counted vmcnt: (NB - 1 - j) (9 + CPW) later operations may still be in
-// flight) and every wave has passed that point (s_barrier). Blocks occupy LDS
-// regions of their own, so no copy waits for a reader. The B fragments are
-// read by inline asm, which the compiler's wait insertion does not see (its
-// own ds_read_b64_tr_b16 would wait for every LDS copy in flight); a ring of
-// DPF steps is in flight ahead of the MFMAs, lgkmcnt counting the reads issued
-// since. The loop issues no scalar loads (they share lgkmcnt) and the block
-// boundaries are scheduling barriers, so the counts hold as written.
-// Measured at config 5 (MI355X, 100-launch graph): 6.75 us against 7.35 us for
-// the four-channel-block-waves form above. Variants that measured no better:
-// 8 waves splitting the blocks in two with an LDS sum (6.97), 32 output
-// channels per workgroup so that 320 of them cover every CU (7.09), the
-// epilogue through an LDS tile with 16-byte stores (7.46), deeper read rings
-// (DPF 5, 7: 7.06, 7.09), copy offsets computed once for all blocks (6.94).
-// What remains is serial per SIMD: 180 MFMAs (2880 cycles) per wave, about
-// 650 VALU instructions (copy offsets, the tap shift, the epilogue) and the
-// store of 3.3 MB.
+// waves, 64 output channels x one output row) reads, per block j, the wave's
+// nine weight fragments and its share of the block's input rows (CPW 1 KB
+// copies, the block padded to 4 KB per wave so that every wave issues the
+// same count): 9 + CPW operations. Blocks 0 and 1 are issued at entry; the
+// operations of block j + 2 are spread over block j's MFMA steps, one per
+// step, so that they queue behind MFMAs instead of holding the wave at entry
+// (a CU's vector memory path takes a wave about 100 cycles per 1 KB
+// operation here, and a block's MFMAs about 1,100 cycles). Block j starts
+// when the wave's own operations of block j have landed (a counted vmcnt:
+// only block j + 1's 9 + CPW, issued during block j - 1, may still be in
+// flight) and every wave has passed that point (s_barrier). Blocks occupy
+// LDS regions of their own, so no copy waits for a reader. The B fragments
+// are read by inline asm, which the compiler's wait insertion does not see
+// (its own ds_read_b64_tr_b16 would wait for every LDS copy in flight); a
+// ring of DPF steps is in flight ahead of the MFMAs, lgkmcnt counting the
+// reads issued since. The loop issues no scalar loads (they share lgkmcnt)
+// and the issue points are scheduling barriers, so the counts hold as
+// written. The MFMA takes the input fragment as A and the weight as B, so a
+// lane's accumulator registers hold four consecutive output columns of one
+// channel (a 16-byte store each).
+// Measured at config 5 (MI355X, 100-launch graph): 6.08-6.15 us; all of
+// every block issued at entry 6.45-6.54 (same runs), the four-channel-block-
+// waves form above 7.35. Per-wave timestamps (cycles, median): entry to the
+// first two blocks issued 2,300, block compute 1,090 (1,400-1,700 with the
+// next block's operations interleaved), the last block plus the tap shift
+// and the epilogue 3,300. Variants that measured no better: 8 waves splitting
+// the blocks in two with an LDS sum (6.97), 32 output channels per workgroup
+// so that 320 of them cover every CU (7.09), the epilogue through an LDS tile
+// (7.46), deeper read rings (DPF 5, 7: 7.06, 7.09), copy offsets computed
+// once for all blocks (6.94).
 namespace cvp {
 template <int NF> struct Geo {
     static constexpr uint32_t ROWB = 32 * NF;              // bytes per staged row (16 NF fp16 columns)
@@ -606,64 +614,59 @@ __device__ __forceinline__ void cv_vm_wait()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// The epilogue from the accumulators: lane (fr, fg) holds output channels
-// co_lane .. +3 at positions 16 f + fr; each store instruction writes 16
-// consecutive positions (64 bytes fp32) of four channels. Residual loads go
-// first (all in flight), then the values and the stores; RES and O16 are
-// template flags, so the straight-line code carries no per-element branches.
-// (Staging the tile through LDS for 16-byte stores measured slower: 7.5
-// against 6.4 us at config 5.)
+// The epilogue from the accumulators: lane (cl, g) holds output channel co
+// (cl = lane % 16 of the wave's 16) at positions 16 f + 4 g .. +3 of each
+// fragment f, so one 16-byte (fp32) or 8-byte (fp16) store writes four
+// consecutive outputs, and each store instruction 16 channels x 64 bytes.
+// Residual loads go first (all in flight), then the values and the stores;
+// RES and O16 are template flags, so the straight-line code carries no
+// per-element branches. (With the channels across the accumulator's
+// registers instead, the same outputs took four 4-byte stores each: 20
+// store instructions per wave, and the epilogue about 2,200 of a wave's
+// 10,500 cycles at config 5.)
 template <int EPI, bool RES, bool O16, int NF>
-__device__ __forceinline__ void conv3_pipe_store(const ConvParams& p, float4v (&acc)[NF], const float (&bias)[4],
-                                                 const float (&sc)[4], uint32_t co_lane, uint32_t ho, uint32_t b,
-                                                 int fr)
+__device__ __forceinline__ void conv3_pipe_store(const ConvParams& p, float4v (&acc)[NF], float bias, float sc,
+                                                 uint32_t co, uint32_t ho, uint32_t b, int g)
 {
-    const bool scaled = p.scale != nullptr, before = p.residual_order == 1;
-    const size_t HoWo = (size_t)p.ho * p.wo;
-    // channels of the lane's four that exist (a lane past Co stores nothing)
-    const uint32_t rows = co_lane < p.co ? min(p.co - co_lane, 4u) : 0u;
-    const size_t o0 = ((size_t)b * p.co + co_lane) * HoWo + (size_t)ho * p.wo + fr;
-    float rr[4][NF];
+    if (co >= p.co) return;
+    const bool before = p.residual_order == 1;
+    const size_t o0 = (((size_t)b * p.co + co) * p.ho + ho) * p.wo + 4 * g;
+    float4v rr[NF];
     if constexpr (RES) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                // (a channel past Co reads the last one; its value is not stored)
-                const size_t o =
-                    ((size_t)b * p.co + min(co_lane + r, p.co - 1)) * HoWo + (size_t)ho * p.wo + fr + 16 * f;
-                rr[r][f] = p.residual_dtype == DT_F16 ? (float)((const half_t*)p.residual)[o]
-                                                      : ((const float*)p.residual)[o];
-            }
+        for (int f = 0; f < NF; ++f)
+            rr[f] = p.residual_dtype == DT_F16
+                        ? __builtin_convertvector(*(const half4*)((const half_t*)p.residual + o0 + 16 * f), float4v)
+                        : *(const float4v*)((const float*)p.residual + o0 + 16 * f);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        if ((uint32_t)r >= rows) break;
+    for (int f = 0; f < NF; ++f) {
+        float4v v;
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            float x = scaled ? fmaf(acc[f][r], sc[r], bias[r]) : acc[f][r] + bias[r];
-            if constexpr (RES) x += before ? rr[r][f] : 0.f;
+        for (int r = 0; r < 4; ++r) {
+            // (sc is 1 without a scale: fma(a, 1, b) is exactly a + b)
+            float x = fmaf(acc[f][r], sc, bias);
+            if constexpr (RES) x += before ? rr[f][r] : 0.f;
             x = cv_act<EPI>(x);
-            if constexpr (RES) x += before ? 0.f : rr[r][f];
-            const size_t o = o0 + (size_t)r * HoWo + 16 * f;
-            if constexpr (O16) ((half_t*)p.out)[o] = (half_t)x;
-            else ((float*)p.out)[o] = x;
+            if constexpr (RES) x += before ? 0.f : rr[f][r];
+            v[r] = x;
         }
+        if constexpr (O16) *(half4*)((half_t*)p.out + o0 + 16 * f) = __builtin_convertvector(v, half4);
+        else *(float4v*)((float*)p.out + o0 + 16 * f) = v;
     }
 }
 
 template <int EPI, int NF>
-__device__ __forceinline__ void conv3_pipe_store_sel(const ConvParams& p, float4v (&acc)[NF], const float (&bias)[4],
-                                                     const float (&sc)[4], uint32_t co_lane, uint32_t ho, uint32_t b,
-                                                     int fr)
+__device__ __forceinline__ void conv3_pipe_store_sel(const ConvParams& p, float4v (&acc)[NF], float bias, float sc,
+                                                     uint32_t co, uint32_t ho, uint32_t b, int g)
 {
     const bool res = p.residual != nullptr, o16 = p.o_dtype == DT_F16;
     if (res) {
-        if (o16) conv3_pipe_store<EPI, true, true>(p, acc, bias, sc, co_lane, ho, b, fr);
-        else conv3_pipe_store<EPI, true, false>(p, acc, bias, sc, co_lane, ho, b, fr);
+        if (o16) conv3_pipe_store<EPI, true, true>(p, acc, bias, sc, co, ho, b, g);
+        else conv3_pipe_store<EPI, true, false>(p, acc, bias, sc, co, ho, b, g);
     } else {
-        if (o16) conv3_pipe_store<EPI, false, true>(p, acc, bias, sc, co_lane, ho, b, fr);
-        else conv3_pipe_store<EPI, false, false>(p, acc, bias, sc, co_lane, ho, b, fr);
+        if (o16) conv3_pipe_store<EPI, false, true>(p, acc, bias, sc, co, ho, b, g);
+        else conv3_pipe_store<EPI, false, false>(p, acc, bias, sc, co, ho, b, g);
     }
 }
 
@@ -683,21 +686,21 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
     const uint32_t co0 = blockIdx.x * 64, ho = blockIdx.y, b = blockIdx.z;
     const int fr = lane & 15, fg = lane >> 4;
     const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.x * 4 + g, CO16 - 1);   // past Co: discarded
-    const uint32_t co_lane = co0 + g * 16 + fg * 4;   // the lane's 4 output channels (accumulator rows)
+    // accumulator layout (the MFMA takes the input as A and the weight as
+    // B): lane (fr, fg) holds output channel co at positions 4 fg .. +3 of
+    // each 16-wide fragment, one per register
+    const uint32_t co = co0 + g * 16 + fr;
 
-    // bias and scale of the lane's channels (a missing one reads the packed
+    // bias and scale of the lane's channel (a missing one reads the packed
     // weight, at least Co values long, and is ignored)
-    float bias[4], sc[4];
+    float bias, sc;
     {
         const half_t* bsrc = p.bias ? (const half_t*)p.bias : p.wp;
         const half_t* ssrc = p.scale ? (const half_t*)p.scale : p.wp;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t co = min(co_lane + r, p.co - 1);
-            const float bv = (float)bsrc[co];   // unconditional: no branch, no early wait
-            bias[r] = p.bias ? bv : 0.f;
-            sc[r] = (float)ssrc[co];
-        }
+        const uint32_t cc = min(co, p.co - 1);
+        const float bv = (float)bsrc[cc], sv = (float)ssrc[cc];   // unconditional: no branch, no early wait
+        bias = p.bias ? bv : 0.f;
+        sc = p.scale ? sv : 1.f;
     }
 
     // Block j: this wave's weight fragments, then its share of the block's
@@ -707,14 +710,13 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
         (void*)((const half_t*)p.x + (size_t)b * p.ci * p.hi * (16 * NF)), (short)0, (int)(p.ci * plane_bytes),
         0x00020000);
     half8 wa[NB][9];
-    static_for<NB>([&](auto J) __attribute__((always_inline)) {
-        constexpr int j = J;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int tap = 0; tap < 9; ++tap)
-            wa[j][tap] = *(const half8*)(p.wp + ((((size_t)tap * CO16 + oblk) * NB + j) * 64 + lane) * 8);
-#pragma unroll
-        for (uint32_t k = 0; k < CPW; ++k) {
+    // operation i of block j (9 + CPW per block): weight fragment i, then copy i - 9
+    auto issue_op = [&](auto J, auto I) __attribute__((always_inline)) {
+        constexpr int j = J, i = I;
+        if constexpr (i < 9) {
+            wa[j][i] = *(const half8*)(p.wp + ((((size_t)i * CO16 + oblk) * NB + j) * 64 + lane) * 8);
+        } else {
+            constexpr uint32_t k = i - 9;
             const uint32_t i0 = (k * NW + (uint32_t)wave) * 1024, pos = i0 + (uint32_t)lane * 16;
             const uint32_t c = j * 32 + pos / CHB, w = pos % CHB, r = w / ROWB;
             const int hi = (int)ho + (int)r - 1;
@@ -724,6 +726,12 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(xs + j * CBB + i0),
                                                      16, (int)off, 0, 0, 0);
         }
+    };
+    constexpr int OPS = 9 + (int)CPW;
+    // blocks 0 and 1 up front; block j + 2 is issued during block j's MFMAs
+    static_for<(NB < 2 ? NB : 2)>([&](auto J) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<OPS>([&](auto I) __attribute__((always_inline)) { issue_op(J, I); });
         __builtin_amdgcn_sched_barrier(0);
     });
 
@@ -738,7 +746,9 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
         (uint32_t)reinterpret_cast<uintptr_t>(xs) + (8 * fg + (fr >> 2)) * CHB + (fr & 3) * 8;
     static_for<NB>([&](auto J) __attribute__((always_inline)) {
         constexpr int j = J;
-        cv_vm_wait<(NB - 1 - j) * (9 + CPW)>();   // this wave's copies of block j have landed
+        // this wave's operations of block j have landed (only block j + 1's,
+        // issued during block j - 1, may be outstanding) ...
+        cv_vm_wait<(j + 1 < NB ? OPS : 0)>();
         __builtin_amdgcn_s_barrier();               // ... and every other wave's
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t base = lbase + j * CBB;
@@ -759,30 +769,49 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
             const half8 bv = __builtin_shufflevector(lo[s], hi[s], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int kw = 0; kw < 3; ++kw)
-                P[kw][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[j][kh * 3 + kw], bv, P[kw][f], 0, 0, 0);
+                P[kw][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bv, wa[j][kh * 3 + kw], P[kw][f], 0, 0, 0);
+            // one operation of block j + 2 per step, so that its loads queue
+            // behind the MFMAs instead of ahead of them
+            if constexpr (j + 2 < NB) {
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (s < OPS) issue_op(std::integral_constant<int, j + 2>{}, SS);
+                if constexpr (s == S - 1 && S < OPS)
+                    static_for<OPS - S>([&](auto I) __attribute__((always_inline)) {
+                        issue_op(std::integral_constant<int, j + 2>{}, std::integral_constant<int, S + I>{});
+                    });
+                __builtin_amdgcn_sched_barrier(0);
+            }
         });
         __builtin_amdgcn_sched_barrier(0);
     });
 
-    // the taps combined: column x of fragment f is lane fr = x of each row
+    // The taps combined: output column x = 16 f + 4 fg + r takes P[1] at x,
+    // P[0] at x - 1 and P[2] at x + 1. Inside a lane's four registers that is
+    // a register index; the first P[0] and the last P[2] term come from the
+    // neighbouring position group (lane -16, resp. +16, mod 64), which for
+    // the fragment's first (last) group is the previous (next) fragment's
+    // last (first) group; past the row's ends they are the zero padding.
+    // Each lane offers the value its neighbour needs, one bpermute each way.
+    const int src_lo = ((lane + 48) & 63) * 4, src_hi = ((lane + 16) & 63) * 4;
     float4v acc[NF];
 #pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float a0 = cv_row_ror<1>(P[0][f][r]);
-            const float e0 = f > 0 ? cv_row_ror<1>(P[0][f > 0 ? f - 1 : 0][r]) : 0.f;
-            const float a2 = cv_row_ror<15>(P[2][f][r]);
-            const float e2 = f + 1 < NF ? cv_row_ror<15>(P[2][f + 1 < NF ? f + 1 : f][r]) : 0.f;
-            acc[f][r] = P[1][f][r] + (fr == 0 ? e0 : a0) + (fr == 15 ? e2 : a2);
-        }
+    for (int f = 0; f < NF; ++f) {
+        const float off0 = fg == 3 ? (f > 0 ? P[0][f > 0 ? f - 1 : 0][3] : 0.f) : P[0][f][3];
+        const float off2 = fg == 0 ? (f + 1 < NF ? P[2][f + 1 < NF ? f + 1 : f][0] : 0.f) : P[2][f][0];
+        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lo, __builtin_bit_cast(int, off0)));
+        const float x2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_hi, __builtin_bit_cast(int, off2)));
+        acc[f][0] = P[1][f][0] + x0 + P[2][f][1];
+        acc[f][1] = P[1][f][1] + P[0][f][0] + P[2][f][2];
+        acc[f][2] = P[1][f][2] + P[0][f][1] + P[2][f][3];
+        acc[f][3] = P[1][f][3] + P[0][f][2] + x2;
+    }
     switch (p.epilogue) {
-    case 1: conv3_pipe_store_sel<1, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
-    case 2: conv3_pipe_store_sel<2, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
-    case 3: conv3_pipe_store_sel<3, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
-    case 4: conv3_pipe_store_sel<4, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
-    case 5: conv3_pipe_store_sel<5, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
-    default: conv3_pipe_store_sel<0, NF>(p, acc, bias, sc, co_lane, ho, b, fr); break;
+    case 1: conv3_pipe_store_sel<1, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 2: conv3_pipe_store_sel<2, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 3: conv3_pipe_store_sel<3, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 4: conv3_pipe_store_sel<4, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 5: conv3_pipe_store_sel<5, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    default: conv3_pipe_store_sel<0, NF>(p, acc, bias, sc, co, ho, b, fg); break;
     }
 }
 

@@ -580,7 +580,11 @@ __global__ __launch_bounds__(CT * 16) __attribute__((amdgpu_waves_per_eu(4))) vo
 // the blocks in two with an LDS sum (6.97), 32 output channels per workgroup
 // so that 320 of them cover every CU (7.09), the epilogue through an LDS tile
 // (7.46), deeper read rings (DPF 5, 7: 7.06, 7.09), copy offsets computed
-// once for all blocks (6.94).
+// once for all blocks (6.94), and four more waves that only load, with the
+// weight fragments through a three-slot LDS ring (6.55: the weights' LDS
+// writes and reads, 72 KB per block, made each block about 1,300 cycles,
+// and a loading wave cannot release a landed block while it is held
+// issuing the next).
 namespace cvp {
 template <int NF> struct Geo {
     static constexpr uint32_t ROWB = 32 * NF;              // bytes per staged row (16 NF fp16 columns)
@@ -667,6 +671,41 @@ __device__ __forceinline__ void conv3_pipe_store_sel(const ConvParams& p, float4
     } else {
         if (o16) conv3_pipe_store<EPI, false, true>(p, acc, bias, sc, co, ho, b, g);
         else conv3_pipe_store<EPI, false, false>(p, acc, bias, sc, co, ho, b, g);
+    }
+}
+
+// The taps combined: output column x = 16 f + 4 fg + r takes P[1] at x,
+// P[0] at x - 1 and P[2] at x + 1. Inside a lane's four registers that is a
+// register index; the first P[0] and the last P[2] term come from the
+// neighbouring position group (lane -16, resp. +16, mod 64), which for the
+// fragment's first (last) group is the previous (next) fragment's last
+// (first) group; past the row's ends they are the zero padding. Each lane
+// offers the value its neighbour needs, one bpermute each way. Then the
+// epilogue.
+template <int NF>
+__device__ __forceinline__ void conv3_taps_store(const ConvParams& p, float4v (&P)[3][NF], float bias, float sc,
+                                                 uint32_t co, uint32_t ho, uint32_t b, int fg, int lane)
+{
+    const int src_lo = ((lane + 48) & 63) * 4, src_hi = ((lane + 16) & 63) * 4;
+    float4v acc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const float off0 = fg == 3 ? (f > 0 ? P[0][f > 0 ? f - 1 : 0][3] : 0.f) : P[0][f][3];
+        const float off2 = fg == 0 ? (f + 1 < NF ? P[2][f + 1 < NF ? f + 1 : f][0] : 0.f) : P[2][f][0];
+        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lo, __builtin_bit_cast(int, off0)));
+        const float x2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_hi, __builtin_bit_cast(int, off2)));
+        acc[f][0] = P[1][f][0] + x0 + P[2][f][1];
+        acc[f][1] = P[1][f][1] + P[0][f][0] + P[2][f][2];
+        acc[f][2] = P[1][f][2] + P[0][f][1] + P[2][f][3];
+        acc[f][3] = P[1][f][3] + P[0][f][2] + x2;
+    }
+    switch (p.epilogue) {
+    case 1: conv3_pipe_store_sel<1, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 2: conv3_pipe_store_sel<2, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 3: conv3_pipe_store_sel<3, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 4: conv3_pipe_store_sel<4, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    case 5: conv3_pipe_store_sel<5, NF>(p, acc, bias, sc, co, ho, b, fg); break;
+    default: conv3_pipe_store_sel<0, NF>(p, acc, bias, sc, co, ho, b, fg); break;
     }
 }
 
@@ -785,34 +824,7 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
         __builtin_amdgcn_sched_barrier(0);
     });
 
-    // The taps combined: output column x = 16 f + 4 fg + r takes P[1] at x,
-    // P[0] at x - 1 and P[2] at x + 1. Inside a lane's four registers that is
-    // a register index; the first P[0] and the last P[2] term come from the
-    // neighbouring position group (lane -16, resp. +16, mod 64), which for
-    // the fragment's first (last) group is the previous (next) fragment's
-    // last (first) group; past the row's ends they are the zero padding.
-    // Each lane offers the value its neighbour needs, one bpermute each way.
-    const int src_lo = ((lane + 48) & 63) * 4, src_hi = ((lane + 16) & 63) * 4;
-    float4v acc[NF];
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-        const float off0 = fg == 3 ? (f > 0 ? P[0][f > 0 ? f - 1 : 0][3] : 0.f) : P[0][f][3];
-        const float off2 = fg == 0 ? (f + 1 < NF ? P[2][f + 1 < NF ? f + 1 : f][0] : 0.f) : P[2][f][0];
-        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lo, __builtin_bit_cast(int, off0)));
-        const float x2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_hi, __builtin_bit_cast(int, off2)));
-        acc[f][0] = P[1][f][0] + x0 + P[2][f][1];
-        acc[f][1] = P[1][f][1] + P[0][f][0] + P[2][f][2];
-        acc[f][2] = P[1][f][2] + P[0][f][1] + P[2][f][3];
-        acc[f][3] = P[1][f][3] + P[0][f][2] + x2;
-    }
-    switch (p.epilogue) {
-    case 1: conv3_pipe_store_sel<1, NF>(p, acc, bias, sc, co, ho, b, fg); break;
-    case 2: conv3_pipe_store_sel<2, NF>(p, acc, bias, sc, co, ho, b, fg); break;
-    case 3: conv3_pipe_store_sel<3, NF>(p, acc, bias, sc, co, ho, b, fg); break;
-    case 4: conv3_pipe_store_sel<4, NF>(p, acc, bias, sc, co, ho, b, fg); break;
-    case 5: conv3_pipe_store_sel<5, NF>(p, acc, bias, sc, co, ho, b, fg); break;
-    default: conv3_pipe_store_sel<0, NF>(p, acc, bias, sc, co, ho, b, fg); break;
-    }
+    conv3_taps_store<NF>(p, P, bias, sc, co, ho, b, fg, lane);
 }
 
 template <int NF, int NB>

@@ -276,7 +276,15 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : (TRI ? 5 : 4)) void scores_kern
 // two classes (256 workgroups, up to 8 computed tiles each) 13.4, eight
 // (1024, two rounds at two per CU) 14.6, the classes of a CU's two units
 // balanced by reversing the second half of the units 11.1-11.2, stores
-// without the non-temporal hint 15.7.
+// without the non-temporal hint 15.7, a fifth wave per workgroup doing every
+// load (Q and the K tiles through LDS, so that the four computing waves never
+// wait on vmcnt, which on this architecture counts their stores too)
+// 10.7-11.1 against 10.7-11.3. Writing S alone in this kernel's store
+// patterns (no loads, no MFMAs; 512 workgroups x four 64x64 tiles) takes 6.8
+// us with the hidden tiles' 16-byte stores and 7.0-7.2 us with the computed
+// tiles' 4-byte stores, against 6.4 us for 32 MiB written in contiguous 16 KB
+// runs per wave: the rest of this kernel's time is the longest strips' Q and K
+// loads ahead of their stores.
 template <int D>
 __global__ __launch_bounds__(256, 2) void scores_strip_kernel(GemmParams p)
 {

@@ -25,7 +25,10 @@
 //    D/32 fragments of 32x32.
 //  * K and V tiles (row-major, 16-byte chunks XOR-swizzled by row) are copied
 //    global -> LDS by buffer_load ... lds, double buffered: the copies of tile
-//    t + 2 are issued as soon as every wave has finished reading tile t.
+//    t + 1 are issued during tile t's S^T MFMAs, a few per MFMA group (issued
+//    as one burst, the wave stalled about 1,200 cycles on the vector memory
+//    path before its next MFMA: 25.9 against 26.4 us per step at config
+//    "attn").
 // Rows with no visible key give 0.
 #include <algorithm>
 
@@ -290,10 +293,9 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // The wave's 32 query rows go straight into VGPRs as the B operand of
     // S^T = K Q^T (lane l: query l % 32, head-dim values 16 s + 8 (l / 32)
     // .. +7 of step s; rows past Tq read as zero through the resource's
-    // range), issued first; then tile 0's copies and tile 1's, so that tile
-    // 1 is in flight during the prologue. Vector loads and the LDS copies
-    // each complete in issue order, so once at most the tile-1 copies are
-    // outstanding, the query rows and tile 0 have landed.
+    // range), issued first; then tile 0's copies. Both are waited for in
+    // full (vmcnt(0)) at the top of tile 0; tile 1's copies go out during
+    // tile 0's S^T MFMAs.
     // fp32 Q is rounded to fp16 here (the reference's f16 staging of Q,
     // attention-fa.comp:335-342 with stagingF16, as its AMD tiles take).
     half8 qf[KS];
@@ -344,18 +346,14 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16, lc = swz<D>(r, pc);
         coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
     }
-    const auto issue = [&](int t) __attribute__((always_inline)) {
-        // (< Tkv: a visible tile starts inside the keys)
-        const uint32_t row0 = __builtin_amdgcn_readfirstlane((uint32_t)(tb + t) * BKV);
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(kh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(vh0 + (size_t)row0 * ROWG), (short)0, (int)((Tkv - row0) * ROWG), 0x00020000);
-        fa_issue<D>(rk, rv, lds, coff, t, wave);
+    // tile t's resources (a visible tile starts inside the keys; a tile past
+    // the unit's last, never copied, is clamped to the last key row)
+    const auto rsrc = [&](int t, const char* h) __attribute__((always_inline)) {
+        const uint32_t row0 = __builtin_amdgcn_readfirstlane(std::min<uint32_t>((uint32_t)(tb + t) * BKV, Tkv - 1));
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(h + (size_t)row0 * ROWG), (short)0,
+                                                 (int)((Tkv - row0) * ROWG), 0x00020000);
     };
-
-    if (ntiles > 0) issue(0);
-    if (ntiles > 1) issue(1);
+    if (ntiles > 0) fa_issue<D>(rsrc(0, kh0), rsrc(0, vh0), lds, coff, 0, wave);
 
     // (the rest of the set-up runs while Q and the first tiles load)
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
@@ -385,14 +383,11 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         vofs[j] = lds0 + (vkey + vrow) * L::ROWB + ((4 * j + (vcol >> 3)) ^ swz_f((vkey + vrow) & 7)) * 16 +
                   (vcol & 7) * 2;
 
-    if (ntiles > 1) fa_wait_vmcnt<2 * L::COPIES>();
-    else fa_wait_vmcnt<0>();
     for (int t = 0; t < ntiles; ++t) {
-        // tile t landed in every wave's share (tile t + 1's copies may be in flight)
-        if (t > 0) {
-            if (t + 1 < ntiles) fa_wait_vmcnt<2 * L::COPIES>();
-            else fa_wait_vmcnt<0>();
-        }
+        // Tile t landed in every wave's share: nothing younger is in flight
+        // (tile t + 1's copies are issued during tile t's S^T MFMAs, a few
+        // per group, so that the wave does not stall on a burst of them).
+        fa_wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         const uint32_t sb = (t & 1) * L::STAGE;
         uint32_t kaddr[NK], vaddr[2];
@@ -407,6 +402,11 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         // chains); K fragments are read in groups of G, the next group's
         // reads in flight behind the current group's MFMAs.
         constexpr int NS = 2 * KS, G = NS < 8 ? NS : (D == 256 ? 4 : 8);
+        constexpr int OPG = 2 * L::COPIES / (NS / G);   // tile t + 1 copies per MFMA group
+        static_assert(OPG * (NS / G) == 2 * L::COPIES, "copies spread evenly over the groups");
+        const bool next = t + 1 < ntiles;
+        const __amdgpu_buffer_rsrc_t rkn = rsrc(t + 1, kh0), rvn = rsrc(t + 1, vh0);
+        LDS_AS char* nst = lds + ((t + 1) & 1) * L::STAGE + wave * L::COPIES * 1024;
         float16v sacc[2] = {(float16v)0.f, (float16v)0.f};
         half8 ka[2][G];
         static_for<G>([&](auto I) __attribute__((always_inline)) { ka[0][I] = fa_kfrag<D, I>(kaddr); });
@@ -427,6 +427,18 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
                 const int idx = gi * G + i;
                 sacc[idx & 1] =
                     __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[cur][i], qf[idx >> 1], sacc[idx & 1], 0, 0, 0);
+            }
+            if (next) {
+                static_for<OPG>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int op = gi * OPG + I;   // K copies, then V copies
+                    constexpr int j = op % L::COPIES;
+                    if constexpr (op < L::COPIES)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rkn, (LDS_AS void*)(nst + j * 1024), 16, (int)coff[j],
+                                                                 0, 0, 0);
+                    else
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rvn, (LDS_AS void*)(nst + L::TILE + j * 1024), 16,
+                                                                 (int)coff[j], 0, 0, 0);
+                });
             }
         });
         // first key step's V^T fragments, read while the softmax runs (after
@@ -536,7 +548,6 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         // every wave is done reading stage t & 1 before tile t + 2 overwrites it
         __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (t + 2 < ntiles) issue(t + 2);
     }
 
     // Output: a partial when the key range is split, else O / l. A partial

@@ -562,19 +562,10 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // 64 lanes x 16 contiguous bytes at a time. The last tile's barrier
     // already saw every wave's reads of the K / V stages; each wave then
     // uses its own 32 QW D bytes (the four regions are exactly the stages).
-    constexpr int CR = D / 4;   // 16-byte fp32 chunks per row
-    LDS_AS float4v* ob = (LDS_AS float4v*)(lds + wave * QW * D * 4);
+    constexpr int CR = D / 4;    // 16-byte fp32 chunks per row
+    constexpr int CH16 = D / 8;  // 16-byte fp16 chunks per row
     const bool partial = p.units != 0, part16 = partial && p.o_dtype == DT_F16;
     const float inv = (partial && !part16) ? 1.0f : (l > 0.f ? 1.0f / l : 0.f);
-#pragma unroll
-    for (int d = 0; d < DF; ++d)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const int c = 8 * d + 2 * q4 + hf;
-            const float4v v = {o[d][4 * q4] * inv, o[d][4 * q4 + 1] * inv, o[d][4 * q4 + 2] * inv,
-                               o[d][4 * q4 + 3] * inv};
-            ob[ql * CR + (c ^ (ql & 15))] = v;
-        }
     const size_t gid = ((size_t)b * p.hq + h) * p.units + unit;
     if (partial && hf == 0) {
         float* wml = p.ws_ml + (gid * BQ + wave * QW + ql) * 2;
@@ -586,15 +577,43 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // row (b Tq + r) Hq + h. One loop per destination, so that no branch sits
     // between the LDS reads and the stores.
     const uint32_t wrow0 = q0 + wave * QW;   // the wave's first query row
-    constexpr int NJ = QW * CR / 64;         // 16-byte chunks per lane
     if (part16) {
+        // fp16 partials go through LDS as fp16 (half the LDS traffic of the
+        // fp32 rows): 8-byte pieces, 16-byte chunk 4 d + q4 of the row at
+        // slot chunk ^ (r % 16) (r % 8 at D = 64), read back as whole chunks
+        LDS_AS half4* obh = (LDS_AS half4*)(lds + wave * QW * D * 4);
+        constexpr int SW16 = CH16 >= 16 ? 15 : CH16 - 1;
+#pragma unroll
+        for (int d = 0; d < DF; ++d)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int c = 4 * d + q4;
+                const float4v v = {o[d][4 * q4] * inv, o[d][4 * q4 + 1] * inv, o[d][4 * q4 + 2] * inv,
+                                   o[d][4 * q4 + 3] * inv};
+                obh[(ql * CH16 + (c ^ (ql & SW16))) * 2 + hf] = __builtin_convertvector(v, half4);
+            }
+        constexpr int NJ16 = QW * CH16 / 64;   // 16-byte chunks per lane
+        const LDS_AS half8* rb = (const LDS_AS half8*)(lds + wave * QW * D * 4);
         half_t* dst = uniform_ptr((half_t*)p.ws_o + (gid * BQ + wave * QW) * D);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int e = j * 64 + lane, r = e / CR, c = e % CR;
-            *(half4*)(dst + r * D + 4 * c) = __builtin_convertvector(ob[r * CR + (c ^ (r & 15))], half4);
+        for (int j = 0; j < NJ16; ++j) {
+            const int e = j * 64 + lane, r = e / CH16, c = e % CH16;
+            *(half8*)(dst + r * D + 8 * c) = rb[r * CH16 + (c ^ (r & SW16))];
         }
-    } else if (partial) {
+        return;
+    }
+    LDS_AS float4v* ob = (LDS_AS float4v*)(lds + wave * QW * D * 4);
+#pragma unroll
+    for (int d = 0; d < DF; ++d)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int c = 8 * d + 2 * q4 + hf;
+            const float4v v = {o[d][4 * q4] * inv, o[d][4 * q4 + 1] * inv, o[d][4 * q4 + 2] * inv,
+                               o[d][4 * q4 + 3] * inv};
+            ob[ql * CR + (c ^ (ql & 15))] = v;
+        }
+    constexpr int NJ = QW * CR / 64;         // 16-byte chunks per lane
+    if (partial) {
         float* dst = uniform_ptr(p.ws_o + (gid * BQ + wave * QW) * D);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {

@@ -182,7 +182,7 @@ __device__ __forceinline__ half8 fa_vfrag(const uint32_t (&vaddr)[2])
 // contiguous range [x q + min(x, r), ..) of the n blocks (q = n / 8,
 // r = n % 8), so that consecutive units -- one head's query tiles and key
 // chunks, which read the same K, V and Q -- share one XCD's L2.
-__device__ __forceinline__ uint32_t fa_xcd_block(uint32_t w, uint32_t n)
+__host__ __device__ inline uint32_t fa_xcd_block(uint32_t w, uint32_t n)
 {
     const uint32_t q = n / 8, r = n % 8, x = w % 8;
     return x * q + (x < r ? x : r) + w / 8;
@@ -250,39 +250,38 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     const int ql = lane & 31, hf = lane >> 5;   // lane's query (of the wave's 32) and lane half
     const uint32_t Tq = p.tq, Tkv = p.tkv;
     const uint32_t nqt = (Tq + BQ - 1) / BQ;
-    // Workgroup -> (unit, head, batch) with the units of one head on one XCD
-    // (fa_xcd_block), then unit -> (query tile, key chunk). Units enumerate
-    // the query tiles from the last (the longest causal walks start first),
-    // chunk by chunk.
-    const uint32_t X = gridDim.x, HX = X * gridDim.y;
-    const uint32_t lb = fa_xcd_block(blockIdx.x + X * (blockIdx.y + gridDim.y * blockIdx.z), HX * gridDim.z);
-    const uint32_t unit = lb % X, h = (lb / X) % gridDim.y, b = lb / HX;
-    uint32_t qt, chunk = 0;
-    if (p.units == 0) {
-        qt = nqt - 1 - unit;
-    } else if (unit < AttnParams::FA_UNIT_TAB) {
-        const uint32_t e = p.unit_tab[unit];   // (the host's walk below, done once per plan)
-        qt = e & 0xFFFFF;
-        chunk = e >> 20;
-    } else {
-        uint32_t u = unit;
-        qt = nqt - 1;
-        for (;;) {
-            const uint32_t nc = fa_chunks(p, qt);
-            if (u < nc || qt == 0) break;
-            u -= nc;
-            --qt;
+    // (every argument the set-up needs, fetched in one batch with the
+    // workgroup's table entry; left alone, the compiler fetches each behind
+    // the branch that first uses it)
+    asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.tq), "s"(p.tkv), "s"(p.head_dim), "s"(p.hq),
+                 "s"(p.hkv), "s"(p.units), "s"(p.q_dtype), "s"(p.chunk_tiles));
+    uint32_t unit, h, b, qt, chunk = 0;
+    if (p.units != 0) {
+        // the plan's table: one entry per workgroup of the 1-D grid
+        const uint32_t e0 = p.wg_tab[2 * blockIdx.x], e1 = p.wg_tab[2 * blockIdx.x + 1];
+        qt = e0 & 0xFFFF;
+        chunk = (e0 >> 16) & 0xFF;
+        unit = e1 & 0x3FF;
+        h = (e1 >> 10) & 0x3FF;
+        b = e1 >> 20;
+        if (chunk == 0 && threadIdx.x == 0) {
+            // the merge pass's index: this query tile's first unit and chunk count
+            uint32_t* tab = p.ws_tab + (((size_t)b * p.hq + h) * nqt + qt) * 2;
+            tab[0] = unit;
+            tab[1] = e0 >> 24;
         }
-        chunk = u;
+    } else {
+        // Workgroup -> (query tile, head, batch) with one head's query
+        // tiles on one XCD (fa_xcd_block), the longest causal walks first.
+        const uint32_t X = gridDim.x, HX = X * gridDim.y;
+        const uint32_t lb = fa_xcd_block(blockIdx.x + X * (blockIdx.y + gridDim.y * blockIdx.z), HX * gridDim.z);
+        unit = lb % X;
+        h = (lb / X) % gridDim.y;
+        b = lb / HX;
+        qt = nqt - 1 - unit;
     }
     qt = __builtin_amdgcn_readfirstlane(qt);
     chunk = __builtin_amdgcn_readfirstlane(chunk);
-    if (p.units != 0 && chunk == 0 && threadIdx.x == 0) {
-        // the merge pass's index: this query tile's first unit and chunk count
-        uint32_t* tab = p.ws_tab + (((size_t)b * p.hq + h) * nqt + qt) * 2;
-        tab[0] = unit;
-        tab[1] = fa_chunks(p, qt);
-    }
     const uint32_t q0 = qt * BQ;
     const uint32_t hk = h / (p.hq / p.hkv);
     const uint32_t qsz = p.q_dtype == DT_F32 ? 4 : 2;
@@ -841,14 +840,26 @@ void attention_plan(AttnParams& p, uint32_t cus)
     for (uint32_t c = min_chunk; c <= key_tiles; ++c) {
         const uint32_t u = attention_units(p, c);
         if (u == 0) return;   // chunks as long as the whole walks: no split
-        if ((uint64_t)u * p.batch * p.hq <= cus) {
+        const uint64_t wgs = (uint64_t)u * p.batch * p.hq;
+        if (wgs <= cus && wgs <= AttnParams::FA_WG_TAB && nqt <= 0x10000) {
             p.chunk_tiles = c;
             p.units = u;
-            // the kernel's unit -> (query tile, chunk) walk, from the last query tile
-            uint32_t n = 0;
-            for (uint32_t qt = nqt; qt-- > 0 && n < AttnParams::FA_UNIT_TAB;)
-                for (uint32_t ch = 0, nc = fa_chunks(p, qt); ch < nc && n < AttnParams::FA_UNIT_TAB; ++ch)
-                    p.unit_tab[n++] = qt | ch << 20;
+            // the units of a head, from the last query tile (the longest
+            // causal walks start first), chunk by chunk
+            uint32_t uq[AttnParams::FA_WG_TAB], uc[AttnParams::FA_WG_TAB], un[AttnParams::FA_WG_TAB], n = 0;
+            for (uint32_t qt = nqt; qt-- > 0;)
+                for (uint32_t ch = 0, nc = fa_chunks(p, qt); ch < nc; ++ch, ++n) {
+                    uq[n] = qt;
+                    uc[n] = ch;
+                    un[n] = nc;
+                }
+            // workgroup w -> unit of head and batch, a head's units on one XCD
+            for (uint32_t w = 0; w < wgs; ++w) {
+                const uint32_t lb = fa_xcd_block(w, (uint32_t)wgs), unit = lb % u, h = (lb / u) % p.hq,
+                               b = lb / (u * p.hq);
+                p.wg_tab[2 * w] = uq[unit] | uc[unit] << 16 | un[unit] << 24;
+                p.wg_tab[2 * w + 1] = unit | h << 10 | b << 20;
+            }
             return;
         }
     }
@@ -896,7 +907,7 @@ static hipError_t attention_launch_d(const AttnParams& p, hipStream_t s)
         if (e != hipSuccess) return e;
     }
     const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
-    const dim3 grid(p.units ? p.units : nqt, p.hq, p.batch);
+    const dim3 grid = p.units ? dim3(p.units * p.hq * p.batch) : dim3(nqt, p.hq, p.batch);
     hipLaunchKernelGGL(attention_fwd_kernel<D>, grid, dim3(256), fa::Lds<D>::BYTES, s, p);
     if (p.units == 0) return hipGetLastError();
     hipError_t e = hipGetLastError();

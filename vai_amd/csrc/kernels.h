@@ -171,10 +171,14 @@ struct AttnParams {
     float* ws_ml;                 // [batch*hq*units][128][2]
     uint32_t* ws_tab;             // [batch*hq*query tiles][2]: first unit, chunks
     void* ws_kv;                  // fp16 copies of fp32 K then V (flash path), else null
-    // unit u -> query tile (low 20 bits) and key chunk (high 12), filled by
-    // attention_plan when units <= FA_UNIT_TAB (else the kernel searches)
-    static constexpr uint32_t FA_UNIT_TAB = 256;
-    uint32_t unit_tab[FA_UNIT_TAB];
+    // Split launches run a 1-D grid of units * hq * batch <= FA_WG_TAB
+    // workgroups (one round on the GPU, a head's units on one XCD), and
+    // attention_plan tabulates what each needs: workgroup w -> [2w] query
+    // tile | key chunk << 16 | the tile's chunk count << 24, [2w + 1] unit |
+    // head << 10 | batch << 20. One scalar load, issued with the kernel's
+    // other argument loads, then no divisions.
+    static constexpr uint32_t FA_WG_TAB = 256;
+    uint32_t wg_tab[2 * FA_WG_TAB];
 };
 bool attention_ok(const AttnParams& p);
 // Units per head for p's shape (0 when no query tile needs splitting), and

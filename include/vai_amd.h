@@ -219,9 +219,10 @@ vai_status vai_attn_scores_launch(const vai_attn_scores_args* args, vai_stream_t
 
 /* ---------------------------------------------------------------------------
  * Attention: O[b,i,h,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h/g,j,:] +
- * mask) V[b,h/g,j,:], g = Hq/Hkv -- the reference's Attention node without a
- * KV cache (/root/reference/vai/nodes/attention.h:77-79, 979-1304;
- * shaders/attention-fa.comp, attention.comp, attention-fa-reduce.comp).
+ * mask) V[b,h/g,j,:], g = Hq/Hkv -- the reference's Attention node, with or
+ * without its KV cache (/root/reference/vai/nodes/attention.h:77-140,
+ * 216-245, 979-1304; shaders/attention-fa.comp, attention.comp,
+ * attention-fa-reduce.comp).
  *   Q [batch,Hq,Tq,D] in q_dtype, K / V [batch,Hkv,Tkv,D] in kv_dtype (f32 or
  *   f16 each, as typeI / typeKV, attention.h:86-88); O token-major
  *   [batch,Tq,Hq,D] in o_dtype (attention-fa.comp:8,96 and attention.h:
@@ -257,6 +258,26 @@ typedef struct {
     uint32_t mask_blocks;                                  /* as vai_attn_scores_args */
     uint32_t mask_bits;
     uint32_t mask_block_end[VAI_MAX_CAUSAL_BLOCKS - 1];
+    /* The KV cache (kvCacheSize / kvCacheDtype / kvCacheRing and the counter,
+     * attention.h:108-140, 216-245, 1003-1023): cache_size = 0 turns it off.
+     * With a cache (batch 1), k_cache / v_cache hold [Hkv, cache_size, D] in
+     * cache_dtype, and cache_count points at a device-readable uint32: the
+     * positions the cache held before this call, read by the kernels when
+     * they run (the reference's kvCacheCount, which the model rewrites before
+     * each forward, so a recorded graph follows it). The call appends its Tkv
+     * new K / V rows at positions count .. count + Tkv - 1 (row p, or
+     * p % cache_size for a ring, whose size must be a multiple of 64), then
+     * attends positions [0, count + Tkv): query i sits at position count +
+     * max(i + Tkv - Tq, 0) and sees up to count + (its mask end among the
+     * new keys), attention-fa.comp:137-146,470-478. K / V may be NULL with
+     * Tkv = 0: the call attends the cache alone. The caller keeps count + Tkv
+     * <= cache_size without a ring, and advances the count itself. */
+    void* k_cache;
+    void* v_cache;
+    const uint32_t* cache_count;
+    uint32_t cache_size;
+    int32_t cache_dtype;          /* VAI_DTYPE_F32 or VAI_DTYPE_F16 */
+    uint32_t cache_ring;
 } vai_attention_args;
 
 vai_status vai_attention_launch(const vai_attention_args* args, vai_stream_t stream);

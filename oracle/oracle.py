@@ -233,6 +233,69 @@ def attention(q, k, v, *, scale=None, causal=False, span=0, out_dtype=np.float32
     return np.ascontiguousarray(np.swapaxes(O, -3, -2)).astype(out_dtype)
 
 
+def _new_token_end(t, tq, causal, blocks):
+    """common/causal_mask.h:25-38: the new tokens query t may read (no mask:
+    all Tq; a causal block: up to itself; a full block: to its end)."""
+    if blocks is None:
+        return t + 1 if causal else tq
+    bits, ends = blocks
+    nb = len(ends) + 1
+    k, end = 0, tq
+    while k + 1 < nb:
+        e = min(ends[k], tq)
+        if t < e:
+            end = e
+            break
+        k += 1
+    return t + 1 if (bits >> (nb - 1 - k)) & 1 else end
+
+
+def attention_cached(q, k, v, k_cache, v_cache, count, *, ring=False, scale=None, causal=False, span=0,
+                     blocks=None, out_dtype=np.float32):
+    """The reference's Attention with its KV cache, restated from its formulas
+    (one sequence): the tkv new K / V rows are appended at positions count ..
+    count + tkv - 1, row p of the cache planes [Hkv, size, D] (p % size for
+    a ring), rounded to the cache dtype (attention-fa.comp:344-400); query t
+    sits at position keyPos(t) = count + max(t + tkv - tq, 0) and reads the
+    positions [keyStart(keyPos(t)), count + keyEnd(t)), keyEnd(t) =
+    max(newTokenEnd(t) + tkv - tq, 0) (attention-fa.comp:137-146, 470-478;
+    causal_mask.h:42-45), position j at its cache row. Exact softmax in
+    float64 as attention() takes it. k / v may be None (tkv = 0). Returns
+    (O token-major [Tq, Hq, D], the updated K cache, the updated V cache)."""
+    q = _c(q)
+    kc, vc = np.array(k_cache, copy=True), np.array(v_cache, copy=True)
+    Hkv, size, D = kc.shape
+    Hq, tq, _ = q.shape[-3:]
+    q = q.reshape(Hq, tq, D)
+    tkv = 0 if k is None else k.shape[-2]
+    for tok in range(tkv):
+        pos = count + tok
+        if not ring and pos >= size:
+            continue
+        row = pos % size if ring else pos
+        kc[:, row] = np.asarray(k, np.float32).reshape(Hkv, tkv, D)[:, tok].astype(kc.dtype)
+        vc[:, row] = np.asarray(v, np.float32).reshape(Hkv, tkv, D)[:, tok].astype(vc.dtype)
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    g = Hq // Hkv
+    O = np.zeros((tq, Hq, D))
+    for t in range(tq):
+        end = count + max(_new_token_end(t, tq, causal, blocks) + tkv - tq, 0)
+        p = count + max(t + tkv - tq, 0)
+        start = 0 if span == 0 or p < span else p + 1 - span
+        js = np.arange(start, end)
+        if js.size == 0:
+            continue
+        rows = js % size if ring else js
+        for h in range(Hq):
+            kk = kc[h // g, rows].astype(np.float64)
+            vv = vc[h // g, rows].astype(np.float64)
+            s = scale * (kk @ q[h, t].astype(np.float64))
+            e = np.exp(s - s.max())
+            O[t, h] = (e @ vv) / e.sum()
+    return O.astype(out_dtype), kc, vc
+
+
 # ---- CPU baseline (cpu_baseline.c): the timed CPU restatement bench.py reports ----
 
 def _f32_or_none(a):

@@ -155,3 +155,89 @@ def test_attention_workspace(gpu):
     q2 = D((32, 1024, 64), np.float16)
     a2 = gpu.attention_args(D((32, 1024, 64), np.float32), q2, q2, q2, causal=True)
     assert gpu.lib().vai_attention_workspace_size(ctypes.byref(a2)) == 0
+
+
+# ---- the KV cache (attention.h:108-140, 1003-1023; attention-fa.comp:
+# 137-146, 344-478): append, then attend positions [0, count + Tkv) ----
+
+def _cache_planes(rng, hkv, size, d, count, ring, dtype):
+    """Cache planes whose rows for positions < count hold data; every other
+    row holds NaN bytes, so that a read past the live keys would show."""
+    kc = np.full((hkv, size, d), np.nan, dtype)
+    vc = kc.copy()
+    for p in range(max(0, count - size) if ring else 0, count):
+        r = p % size if ring else p
+        kc[:, r] = draw((hkv, d), rng, dtype)
+        vc[:, r] = draw((hkv, d), rng, dtype)
+    return kc, vc
+
+
+@pytest.mark.parametrize("d, hq, hkv, tq, tkv, count, size, ring, causal, span, cdt, kdt, qdt", [
+    (128, 4, 2, 200, 200, 0, 512, False, True, 0, np.float16, np.float16, np.float16),    # prefill, empty cache
+    (128, 4, 2, 1, 1, 300, 512, False, True, 0, np.float16, np.float16, np.float16),      # decode
+    (256, 8, 8, 1, 1, 1000, 1024, False, True, 0, np.float16, np.float16, np.float16),    # decode, long cache
+    (128, 4, 4, 48, 48, 100, 256, False, True, 0, np.float16, np.float16, np.float16),    # a prompt chunk
+    (64, 4, 2, 1, 1, 700, 256, True, True, 200, np.float16, np.float16, np.float16),      # ring, sliding window
+    (64, 4, 2, 16, 16, 600, 256, True, True, 128, np.float16, np.float16, np.float16),    # ring, chunk
+    (128, 4, 2, 3, 0, 50, 128, False, False, 0, np.float16, np.float16, np.float16),      # cache alone
+    (64, 2, 1, 5, 5, 77, 128, False, True, 0, np.float32, np.float32, np.float32),        # fp32 cache and inputs
+    (64, 8, 2, 1, 1, 513, 1024, False, True, 0, np.float16, np.float32, np.float32),      # fp32 K / V into fp16
+    (20, 2, 2, 2, 2, 30, 64, False, True, 0, np.float16, np.float16, np.float16),         # plain kernel
+])
+def test_attention_kv_cache(gpu, d, hq, hkv, tq, tkv, count, size, ring, causal, span, cdt, kdt, qdt):
+    rng = np.random.default_rng(count + tq)
+    kc, vc = _cache_planes(rng, hkv, size, d, count, ring, cdt)
+    q = draw((1, hq, tq, d), rng, qdt)
+    k = draw((1, hkv, tkv, d), rng, kdt) if tkv else None
+    v = draw((1, hkv, tkv, d), rng, kdt) if tkv else None
+    D = gpu.DeviceArray.from_numpy
+    dkc, dvc = D(kc), D(vc)
+    cnt = D(np.array([count], np.uint32))
+    out = gpu.DeviceArray((1, tq, hq, d), np.float32)
+    print(f"kv cache d={d} hq={hq} hkv={hkv} tq={tq} tkv={tkv} count={count} size={size} ring={ring}", flush=True)
+    got = gpu.attention(out, D(q), None if k is None else D(k), None if v is None else D(v), causal=causal, span=span,
+                        cache=(dkc, dvc, cnt, ring)).numpy()
+    want, wkc, wvc = oracle.attention_cached(q[0], k, v, kc, vc, count, ring=ring, causal=causal, span=span)
+    assert_close(got[0], want, NAIVE if d % 8 else FP16)
+    # the appended rows hold the new K / V in the cache dtype, every other row is as it was
+    gkc, gvc = dkc.numpy(), dvc.numpy()
+    np.testing.assert_array_equal(gkc, wkc)
+    np.testing.assert_array_equal(gvc, wvc)
+    assert int(cnt.numpy()[0]) == count   # the caller advances the count
+
+
+def test_attention_kv_cache_decode_steps(gpu):
+    """Decode as a model runs it: one token per call, the count advanced on
+    the device between calls; each step matches the reference's formulas over
+    the cache the earlier steps left."""
+    rng = np.random.default_rng(5)
+    hq, hkv, d, size, count = 8, 4, 128, 256, 40
+    kc, vc = _cache_planes(rng, hkv, size, d, count, False, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    dkc, dvc = D(kc), D(vc)
+    cnt = gpu.DeviceArray((1,), np.uint32)
+    for step in range(3):
+        gpu.lib().vai_memcpy_h2d(cnt.ptr, np.array([count], np.uint32).ctypes.data, 4, None)
+        q = draw((1, hq, 1, d), rng, np.float16)
+        k = draw((1, hkv, 1, d), rng, np.float16)
+        v = draw((1, hkv, 1, d), rng, np.float16)
+        out = gpu.DeviceArray((1, 1, hq, d), np.float32)
+        got = gpu.attention(out, D(q), D(k), D(v), causal=True, cache=(dkc, dvc, cnt, False)).numpy()
+        want, kc, vc = oracle.attention_cached(q[0], k, v, kc, vc, count, causal=True)
+        assert_close(got[0], want, FP16)
+        count += 1
+    np.testing.assert_array_equal(dkc.numpy(), kc)
+
+
+def test_attention_kv_cache_rejects(gpu):
+    D = gpu.DeviceArray
+    q, k = D((1, 4, 2, 64), np.float16), D((1, 2, 2, 64), np.float16)
+    kc, cnt = D((2, 100, 64), np.float16), D((1,), np.uint32)
+    out = D((1, 2, 4, 64), np.float32)
+    a = gpu.attention_args(out, q, k, k, cache=(kc, kc, cnt, True))      # ring of 100 rows: not a multiple of 64
+    assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1002
+    q2 = D((2, 4, 2, 64), np.float16)
+    k2 = D((2, 2, 2, 64), np.float16)
+    out2 = D((2, 2, 4, 64), np.float32)
+    a = gpu.attention_args(out2, q2, k2, k2, cache=(kc, kc, cnt, False))  # one counter: batch 1 only
+    assert gpu.lib().vai_attention_launch(ctypes.byref(a), None) == 1002

@@ -134,3 +134,40 @@ def test_attention_argument_checks_need_no_gpu():
     # fp16 K / V at head dim 20 (not a multiple of 8): the plain kernel, no workspace
     a.head_dim, a.kv_dtype = 20, 1
     assert lib.vai_attention_workspace_size(ctypes.byref(a)) == 0
+
+
+def test_attention_kv_cache_argument_checks_need_no_gpu():
+    """The KV cache fields (attention.h:216-245, 959-1023): a cache needs its
+    planes and counter, fp32 / fp16, one sequence, a ring of whole 64-row
+    tiles, and room for the new rows; K / V may be absent (Tkv = 0) only with
+    a cache. The workspace of an fp32 cache at a flash head dim covers fp16
+    copies of the whole planes (the count is only known when the kernels run)."""
+    lib = _capi.lib()
+    a = _capi.AttentionArgs()
+    a.out = a.q = a.k = a.v = 256
+    a.batch, a.hq, a.hkv, a.tq, a.tkv, a.head_dim = 1, 4, 2, 1, 1, 64
+    a.q_dtype, a.kv_dtype, a.o_dtype = 1, 1, 0
+    a.cache_size, a.cache_dtype = 128, 1
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1001   # no planes, no counter
+    a.k_cache = a.v_cache = a.cache_count = 512
+    a.cache_dtype = 5
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1003
+    a.cache_dtype = 0
+    a.batch = 2
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1002   # one counter, one sequence
+    a.batch, a.cache_ring = 1, 1
+    assert lib.vai_attention_workspace_size(ctypes.byref(a)) > 0       # a ring of 128 rows is two tiles: fine ...
+    a.cache_size = 100
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1002   # ... 100 is not a whole number of tiles
+    a.cache_size, a.cache_ring, a.tkv = 128, 0, 200
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1002   # 200 new rows do not fit 128
+    # fp32 planes [2, 128, 64] at a flash head dim: fp16 copies, 2 x 2 x 128 x 64 x 2 bytes
+    a.tkv = 1
+    assert lib.vai_attention_workspace_size(ctypes.byref(a)) % 256 == 0
+    assert lib.vai_attention_workspace_size(ctypes.byref(a)) >= 2 * 2 * 128 * 64 * 2
+    # K / V absent: fine with a cache (Tkv = 0), refused without one
+    a.k = a.v = None
+    a.tkv = 0
+    assert lib.vai_attention_workspace_size(ctypes.byref(a)) > 0
+    a.cache_size = 0
+    assert lib.vai_attention_launch(ctypes.byref(a), None) == 1001

@@ -298,3 +298,63 @@ def test_linear_node_acc16(gpu):
     got = forward(net, {"in0": x})
     assert net.node.plan.startswith("tile_f16")
     assert_close(got, oracle.linear(x, w, b, stage="tile"), FP32)
+
+
+def test_attention_node_kv_cache(gpu):
+    """The Attention node with its KV cache, run as a decoder runs it
+    (attention.h:108-140, 242-246): a prompt, then one-token steps, the model
+    rewriting the counter before each forward. The second one-token forward
+    has the first's shapes, so it replays the recorded launches: the count the
+    kernels read is the live one. Each output matches the reference's
+    formulas over the cache the earlier forwards left, and the node's cache
+    holds every appended K / V row."""
+    pv = pyvai()
+    rng = np.random.default_rng(21)
+    hq, hkv, d, size = 8, 4, 128, 256
+    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d, num_kv_heads=hkv, kv_cache_size=size,
+                                                   kv_cache_dtype=pv.Dtype.F16), ["Q", "K", "V"], {})
+    net.node.set_causal_mask(1, [])
+    counter = gpu.DeviceArray((1,), np.uint32)
+    net.node.set_kv_cache_counter(counter.ptr)
+    kc = np.full((hkv, size, d), np.nan, np.float16)
+    vc = kc.copy()
+    count = 0
+    for t in (20, 1, 1, 3):
+        gpu.lib().vai_memcpy_h2d(counter.ptr, np.array([count], np.uint32).ctypes.data, 4, None)
+        q = draw((1, hq, t, d), rng, np.float16)
+        k = draw((1, hkv, t, d), rng, np.float16)
+        v = draw((1, hkv, t, d), rng, np.float16)
+        print(f"kv cache node: count {count}, {t} new tokens", flush=True)
+        got = forward(net, {"Q": q, "K": k, "V": v}).astype(np.float32)
+        want, kc, vc = oracle.attention_cached(q[0], k, v, kc, vc, count, causal=True)
+        assert_close(got[0], want, FP16)
+        count += t
+    np.testing.assert_array_equal(net.node["K_cache"].to_numpy()[:, :count], kc[:, :count])
+    np.testing.assert_array_equal(net.node["V_cache"].to_numpy()[:, :count], vc[:, :count])
+
+
+def test_attention_node_kv_cache_alone_and_ring(gpu):
+    """K / V unwired: the node attends the cache alone (Tkv = 0,
+    attention.h:1001-1004); a ring rounds its size up to 256 (kvRingAlign)."""
+    pv = pyvai()
+    rng = np.random.default_rng(22)
+    hq, d = 4, 64
+    ring = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d, kv_cache_size=100,
+                                                    kv_cache_dtype=pv.Dtype.F16, kv_cache_ring=True), ["Q", "K", "V"], {})
+    assert ring.node.kv_cache_size == 256
+    assert ring.node["K_cache"].shape == [hq, 256, d]
+    net = build_net(lambda: pv.nodes.AttentionNode(num_q_heads=hq, head_dim=d, kv_cache_size=64,
+                                                   kv_cache_dtype=pv.Dtype.F32), ["Q"], {})
+    counter = gpu.DeviceArray.from_numpy(np.array([0], np.uint32))
+    net.node.set_kv_cache_counter(counter.ptr)
+    # the cache planes set directly (a persistent slot, uploaded at the next
+    # forward), then a forward that attends 37 cached rows
+    kc = draw((hq, 64, d), rng, np.float32)
+    vc = draw((hq, 64, d), rng, np.float32)
+    net.node["K_cache"] = pv.Tensor.from_numpy(kc)
+    net.node["V_cache"] = pv.Tensor.from_numpy(vc)
+    gpu.lib().vai_memcpy_h2d(counter.ptr, np.array([37], np.uint32).ctypes.data, 4, None)
+    q = draw((1, hq, 2, d), rng, np.float16)
+    got = forward(net, {"Q": q}).astype(np.float32)
+    want, _, _ = oracle.attention_cached(q[0], None, None, kc, vc, 37)
+    assert_close(got[0], want, FP16)

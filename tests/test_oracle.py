@@ -469,3 +469,71 @@ def test_acc16_nan_chain_stays_nan():
     out = oracle.linear_acc16(x, w)
     assert np.isnan(out[0, 0])
     assert out[1, 0] == 65504.0
+
+
+# ---- the KV-cache restatement (oracle.attention_cached) against the plain
+# attention oracle where the reference's formulas reduce to it ----
+
+def _cache_case(rng, hkv, size, d, positions, dtype=np.float32):
+    """A cache plane pair holding the given positions' rows of a key history."""
+    kc = np.full((hkv, size, d), np.nan, dtype)
+    return kc, kc.copy()
+
+
+def test_attention_cached_empty_cache_is_plain_attention():
+    """count = 0: keyEnd and keyPos are the plain end-aligned rule, whatever
+    Tq and Tkv are (attention-fa.comp:137-146)."""
+    rng = np.random.default_rng(11)
+    for tq, tkv, causal, span in [(5, 5, True, 0), (3, 7, True, 0), (7, 3, True, 0), (4, 4, False, 0), (6, 6, True, 3)]:
+        q = rng.standard_normal((4, tq, 16)).astype(np.float32)
+        k = rng.standard_normal((2, tkv, 16)).astype(np.float32)
+        v = rng.standard_normal((2, tkv, 16)).astype(np.float32)
+        kc, vc = _cache_case(rng, 2, 32, 16, [])
+        got, kc2, vc2 = oracle.attention_cached(q, k, v, kc, vc, 0, causal=causal, span=span)
+        np.testing.assert_allclose(got, oracle.attention(q, k, v, causal=causal, span=span), rtol=1e-6, atol=1e-6)
+        assert np.array_equal(kc2[:, :tkv], k) and np.array_equal(vc2[:, :tkv], v)
+        assert np.isnan(kc2[:, tkv:]).all()   # rows past the append untouched
+
+
+def test_attention_cached_is_attention_over_the_key_history():
+    """Tq <= Tkv: query t sits at count + t + Tkv - Tq, the end alignment of
+    plain attention over the count + Tkv keys of the whole history."""
+    rng = np.random.default_rng(12)
+    for tq, tkv, count, causal, span in [(2, 3, 10, True, 0), (1, 1, 20, True, 0), (4, 4, 7, False, 0),
+                                         (3, 3, 9, True, 5)]:
+        hk = rng.standard_normal((2, count + tkv, 16)).astype(np.float32)
+        hv = rng.standard_normal((2, count + tkv, 16)).astype(np.float32)
+        kc, vc = _cache_case(rng, 2, 32, 16, [])
+        kc[:, :count], vc[:, :count] = hk[:, :count], hv[:, :count]
+        q = rng.standard_normal((4, tq, 16)).astype(np.float32)
+        got, kc2, _ = oracle.attention_cached(q, hk[:, count:], hv[:, count:], kc, vc, count, causal=causal, span=span)
+        np.testing.assert_allclose(got, oracle.attention(q, hk, hv, causal=causal, span=span), rtol=1e-6, atol=1e-6)
+        assert np.array_equal(kc2[:, :count + tkv], hk)
+
+
+def test_attention_cached_ring_is_the_windowed_history():
+    """A ring of 16 rows holding the last 16 positions (row p % 16) under an
+    8-key window gives what plain windowed attention over the whole history
+    gives."""
+    rng = np.random.default_rng(13)
+    size, count, tkv, tq, span = 16, 37, 2, 2, 8
+    hk = rng.standard_normal((2, count + tkv, 16)).astype(np.float32)
+    hv = rng.standard_normal((2, count + tkv, 16)).astype(np.float32)
+    kc, vc = _cache_case(rng, 2, size, 16, [])
+    for p in range(count - size, count):
+        kc[:, p % size], vc[:, p % size] = hk[:, p], hv[:, p]
+    q = rng.standard_normal((4, tq, 16)).astype(np.float32)
+    got, kc2, _ = oracle.attention_cached(q, hk[:, count:], hv[:, count:], kc, vc, count, ring=True, causal=True,
+                                          span=span)
+    np.testing.assert_allclose(got, oracle.attention(q, hk, hv, causal=True, span=span), rtol=1e-6, atol=1e-6)
+    assert np.array_equal(kc2[:, count % size], hk[:, count])
+
+
+def test_attention_cached_without_new_keys_reads_the_cache():
+    """Tkv = 0: every query sits past the last cached key and reads them all."""
+    rng = np.random.default_rng(14)
+    kc = rng.standard_normal((2, 16, 16)).astype(np.float32)
+    vc = rng.standard_normal((2, 16, 16)).astype(np.float32)
+    q = rng.standard_normal((4, 3, 16)).astype(np.float32)
+    got, _, _ = oracle.attention_cached(q, None, None, kc, vc, 9, causal=True)
+    np.testing.assert_allclose(got, oracle.attention(q, kc[:, :9], vc[:, :9]), rtol=1e-6, atol=1e-6)

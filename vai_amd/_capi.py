@@ -83,6 +83,8 @@ class AttentionArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("mask_blocks", ctypes.c_uint32), ("mask_bits", ctypes.c_uint32),
         ("mask_block_end", ctypes.c_uint32 * (MAX_CAUSAL_BLOCKS - 1)),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p), ("cache_count", ctypes.c_void_p),
+        ("cache_size", ctypes.c_uint32), ("cache_dtype", ctypes.c_int32), ("cache_ring", ctypes.c_uint32),
     ]
 
 
@@ -369,20 +371,31 @@ def attn_scores(scores, q, k, stream=None, **kw):
     return scores
 
 
-def attention_args(out, q, k, v, *, scale=None, causal=False, span=0, blocks=None):
-    """O token-major [..., Tq, Hq, D]; no mask unless causal / blocks ask for one."""
+def attention_args(out, q, k, v, *, scale=None, causal=False, span=0, blocks=None, cache=None):
+    """O token-major [..., Tq, Hq, D]; no mask unless causal / blocks ask for one.
+    cache = (k_cache, v_cache, count, ring): the KV cache planes [Hkv, size, D]
+    (DeviceArrays of one dtype) and a device uint32 DeviceArray holding the
+    positions they held before the call; k / v may then be None (Tkv = 0)."""
     Hq, Tq, D = q.shape[-3:]
-    Hkv, Tkv, _ = k.shape[-3:]
     a = AttentionArgs()
-    a.out, a.q, a.k, a.v = out.ptr, q.ptr, k.ptr, v.ptr
-    a.o_dtype, a.q_dtype, a.kv_dtype = out.code, q.code, k.code
+    a.out, a.q = out.ptr, q.ptr
+    a.o_dtype, a.q_dtype = out.code, q.code
     a.batch = int(np.prod(q.shape[:-3]))
+    if k is not None:
+        Hkv, Tkv, _ = k.shape[-3:]
+        a.k, a.v, a.kv_dtype = k.ptr, v.ptr, k.code
+    else:
+        Hkv, Tkv = cache[0].shape[-3], 0
     a.hq, a.hkv, a.tq, a.tkv, a.head_dim = Hq, Hkv, Tq, Tkv, D
     a.scale = 0.0 if scale is None else float(scale)
     a.causal = 1 if causal else 0
     a.span = span
     _set_blocks(a, blocks)
-    a._keep = (out, q, k, v)
+    if cache is not None:
+        kc, vc, count, ring = cache
+        a.k_cache, a.v_cache, a.cache_count = kc.ptr, vc.ptr, count.ptr
+        a.cache_size, a.cache_dtype, a.cache_ring = kc.shape[-2], kc.code, 1 if ring else 0
+    a._keep = (out, q, k, v, cache)
     return a
 
 

@@ -188,20 +188,22 @@ __host__ __device__ inline uint32_t fa_xcd_block(uint32_t w, uint32_t n)
     return x * q + (x < r ? x : r) + w / 8;
 }
 
-// The 64-key tiles query tile qt can see: [tb, te).
-__host__ __device__ inline void fa_tile_range(const AttnParams& p, uint32_t qt, int64_t& tb, int64_t& te)
+// The 64-key tiles query tile qt can see: [tb, te), in global key positions
+// (a KV cache holding `cached` positions ahead of the new keys).
+__host__ __device__ inline void fa_tile_range(const AttnParams& p, uint32_t qt, uint32_t cached, int64_t& tb,
+                                              int64_t& te)
 {
     const uint32_t q0 = qt * fa::BQ, q1 = std::min<uint32_t>(q0 + fa::BQ, p.tq) - 1;
-    const int64_t kend = p.mask.key_end(q1), kbeg = p.mask.key_start(q0);
+    const int64_t kend = p.mask.key_end_cached(q1, cached), kbeg = p.mask.key_start_cached(q0, cached);
     tb = kbeg / fa::BKV;
     te = kend <= kbeg ? tb : (kend + fa::BKV - 1) / fa::BKV;
 }
 
 // Chunks of query tile qt (at least one, so that every tile writes output).
-__host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt)
+__host__ __device__ inline uint32_t fa_chunks(const AttnParams& p, uint32_t qt, uint32_t cached)
 {
     int64_t tb, te;
-    fa_tile_range(p, qt, tb, te);
+    fa_tile_range(p, qt, cached, tb, te);
     const int64_t n = te - tb;   // at most Tkv / 64: a 32-bit division suffices
     return n <= 0 ? 1u : ((uint32_t)n + p.chunk_tiles - 1) / p.chunk_tiles;
 }
@@ -248,7 +250,12 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ql = lane & 31, hf = lane >> 5;   // lane's query (of the wave's 32) and lane half
-    const uint32_t Tq = p.tq, Tkv = p.tkv;
+    const uint32_t Tq = p.tq;
+    // keys: positions [0, live); with a cache, its count is read here, at run time
+    const uint32_t cached = p.cache_count ? __builtin_amdgcn_readfirstlane(*p.cache_count) : 0u;
+    // (a cache without a ring holds kv_rows positions; the caller keeps the
+    // count within it, and the clamp keeps a violation inside the buffers)
+    const uint32_t KR = p.kv_rows, live = p.ring ? cached + p.tkv : std::min(cached + p.tkv, KR);
     const uint32_t nqt = (Tq + BQ - 1) / BQ;
     // (every argument the set-up needs, fetched in one batch with the
     // workgroup's table entry; left alone, the compiler fetches each behind
@@ -324,7 +331,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
 
     // visible key tiles of the query tile, then this unit's chunk of them
     int64_t tb, te;
-    fa_tile_range(p, qt, tb, te);
+    fa_tile_range(p, qt, cached, tb, te);
     if (p.units != 0) {
         const int64_t c0 = tb + (int64_t)chunk * p.chunk_tiles;
         te = std::min<int64_t>(te, c0 + p.chunk_tiles);
@@ -336,8 +343,8 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
     // lane l's 16 bytes land at physical chunk pc of row r and come from
     // logical chunk swz<D>(r, pc) of that row (the swizzle is its own inverse).
     // (a chunk past the head dim points at byte 2^31, beyond any range)
-    const char* kh0 = uniform_ptr((const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * Tkv * HD));
-    const char* vh0 = uniform_ptr((const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * Tkv * HD));
+    const char* kh0 = uniform_ptr((const char*)((const half_t*)p.k + ((size_t)b * p.hkv + hk) * KR * HD));
+    const char* vh0 = uniform_ptr((const char*)((const half_t*)p.v + ((size_t)b * p.hkv + hk) * KR * HD));
     uint32_t coff[L::COPIES];
 #pragma unroll
     for (int j = 0; j < L::COPIES; ++j) {
@@ -345,19 +352,25 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         const int r = byte / L::ROWB, pc = (byte % L::ROWB) / 16, lc = swz<D>(r, pc);
         coff[j] = 8u * lc < HD ? (uint32_t)(r * ROWG + lc * 16) : 0x80000000u;
     }
-    // tile t's resources (a visible tile starts inside the keys; a tile past
-    // the unit's last, never copied, is clamped to the last key row)
+    // Tile t's resources: they start at the tile's first key row and end at
+    // the last live key (rows past it read as zero, not as stale cache rows)
+    // or the plane's end. A ring holds position j at row j % KR, and KR is a
+    // multiple of 64, so no tile wraps. A tile past the unit's last (never
+    // copied) gets an empty range.
     const auto rsrc = [&](int t, const char* h) __attribute__((always_inline)) {
-        const uint32_t row0 = __builtin_amdgcn_readfirstlane(std::min<uint32_t>((uint32_t)(tb + t) * BKV, Tkv - 1));
-        return __builtin_amdgcn_make_buffer_rsrc((void*)(h + (size_t)row0 * ROWG), (short)0,
-                                                 (int)((Tkv - row0) * ROWG), 0x00020000);
+        const uint32_t j0 = __builtin_amdgcn_readfirstlane((uint32_t)(tb + t) * BKV);
+        const uint32_t row0 = j0 < live ? (p.ring ? j0 % KR : j0) : 0u;
+        const uint32_t rows = j0 < live ? std::min(live - j0, KR - row0) : 0u;
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(h + (size_t)row0 * ROWG), (short)0, (int)(rows * ROWG),
+                                                 0x00020000);
     };
     if (ntiles > 0) fa_issue<D>(rsrc(0, kh0), rsrc(0, vh0), lds, coff, 0, wave);
 
     // (the rest of the set-up runs while Q and the first tiles load)
     const float sl2 = p.scale * 1.4426950408889634f;   // scores in log2 units
     const uint32_t qclip = qrow < Tq ? qrow : Tq - 1;
-    const int64_t row_kend = p.mask.key_end(qclip), row_kbeg = p.mask.key_start(qclip);
+    const int64_t row_kend = std::min<int64_t>(p.mask.key_end_cached(qclip, cached), live);
+    const int64_t row_kbeg = p.mask.key_start_cached(qclip, cached);
     float m = -__builtin_inff(), l = 0.f;
     float16v o[DF];
 #pragma unroll
@@ -718,13 +731,21 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
     }
 }
 
+// The cache count a plan is sized for: the most a launch can see (a full
+// cache; a ring's visible keys span no more than that either), 0 without one.
+// A launch with fewer cached keys runs the same units, some of them empty.
+static uint32_t plan_cached(const AttnParams& p)
+{
+    return p.cache_count && p.kv_rows > p.tkv ? p.kv_rows - p.tkv : 0u;
+}
+
 uint32_t attention_units(const AttnParams& p, uint32_t chunk_tiles)
 {
     AttnParams q = p;
     q.chunk_tiles = chunk_tiles;
-    const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
+    const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ, cached = plan_cached(p);
     uint32_t units = 0;
-    for (uint32_t qt = 0; qt < nqt; ++qt) units += fa_chunks(q, qt);
+    for (uint32_t qt = 0; qt < nqt; ++qt) units += fa_chunks(q, qt, cached);
     return units == nqt ? 0u : units;
 }
 
@@ -760,9 +781,13 @@ __global__ __launch_bounds__(256) void attention_naive_kernel(AttnParams p)
     const uint32_t i = blockIdx.x, h = blockIdx.y, b = blockIdx.z, t = threadIdx.x;
     const uint32_t HD = p.head_dim, hk = h / (p.hq / p.hkv);
     const size_t qbase = (((size_t)b * p.hq + h) * p.tq + i) * HD;
-    const size_t kvbase = ((size_t)b * p.hkv + hk) * p.tkv * HD;
+    const size_t kvbase = ((size_t)b * p.hkv + hk) * p.kv_rows * HD;
     for (uint32_t d = t; d < HD; d += 256) qs[d] = ld(p.q, p.q_dtype, qbase + d);
-    const int64_t kbeg = p.mask.key_start(i), kend = p.mask.key_end(i);
+    const uint32_t cached = p.cache_count ? *p.cache_count : 0u;
+    const int64_t live = p.ring ? (int64_t)cached + p.tkv : std::min<int64_t>((int64_t)cached + p.tkv, p.kv_rows);
+    const int64_t kbeg = p.mask.key_start_cached(i, cached);
+    const int64_t kend = std::min<int64_t>(p.mask.key_end_cached(i, cached), live);
+    const auto krow = [&](int64_t j) -> size_t { return p.ring ? (size_t)(j % p.kv_rows) : (size_t)j; };
     float o[NAIVE_COLS];
 #pragma unroll
     for (int r = 0; r < NAIVE_COLS; ++r) o[r] = 0.f;
@@ -773,7 +798,8 @@ __global__ __launch_bounds__(256) void attention_naive_kernel(AttnParams p)
         float sc = -__builtin_inff();
         if (j < kend) {
             float acc = 0.f;
-            for (uint32_t d = 0; d < HD; ++d) acc = fmaf(qs[d], ld(p.k, p.kv_dtype, kvbase + (size_t)j * HD + d), acc);
+            const size_t kr = kvbase + krow(j) * HD;
+            for (uint32_t d = 0; d < HD; ++d) acc = fmaf(qs[d], ld(p.k, p.kv_dtype, kr + d), acc);
             sc = acc * p.scale;
         }
         const float mnew = fmaxf(m, naive_block_reduce(sc, true, red));   // finite: the tile has a key
@@ -789,7 +815,7 @@ __global__ __launch_bounds__(256) void attention_naive_kernel(AttnParams p)
             if (d >= HD) break;
             float acc = o[r] * alpha;
             for (int64_t jj = 0; jj < n; ++jj)
-                acc = fmaf(ps[jj], ld(p.v, p.kv_dtype, kvbase + (size_t)(j0 + jj) * HD + d), acc);
+                acc = fmaf(ps[jj], ld(p.v, p.kv_dtype, kvbase + krow(j0 + jj) * HD + d), acc);
             o[r] = acc;
         }
         __syncthreads();   // ps is rewritten by the next tile
@@ -800,6 +826,25 @@ __global__ __launch_bounds__(256) void attention_naive_kernel(AttnParams p)
     for (int r = 0; r < NAIVE_COLS; ++r) {
         const uint32_t d = t + 256 * r;
         if (d < HD) st(p.out, p.o_dtype, obase + d, o[r] * inv);
+    }
+}
+
+// The KV cache append (the reference's fused append, attention-fa.comp:
+// 344-400): the tkv new K / V rows of KV head blockIdx.y go to positions
+// cached .. cached + tkv - 1 of the cache (row p, or p % kv_rows for a ring),
+// converted to the cache dtype. A cache without a ring drops rows past its
+// size (the caller keeps the count within it).
+__global__ __launch_bounds__(256) void attention_append_kernel(AttnParams p)
+{
+    const uint32_t HD = p.head_dim, hk = blockIdx.y, cached = *p.cache_count;
+    const size_t n = (size_t)p.tkv * HD;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
+        const uint32_t tok = (uint32_t)(e / HD), d = (uint32_t)(e % HD), pos = cached + tok;
+        if (!p.ring && pos >= p.kv_rows) continue;
+        const size_t row = p.ring ? pos % p.kv_rows : pos;
+        const size_t src = ((size_t)hk * p.tkv + tok) * HD + d, dst = ((size_t)hk * p.kv_rows + row) * HD + d;
+        st((void*)p.k, p.kv_dtype, dst, ld(p.k_new, p.new_dtype, src));
+        st((void*)p.v, p.kv_dtype, dst, ld(p.v_new, p.new_dtype, src));
     }
 }
 
@@ -829,11 +874,11 @@ void attention_plan(AttnParams& p, uint32_t cus)
     // and buffer ranges under 2^31 bytes; anything else takes the plain path.
     const bool flash = HD % 8 == 0 && HD >= 16 && HD <= 256 && ((uintptr_t)p.q % 16) == 0 &&
                        ((uintptr_t)p.k % 16) == 0 && ((uintptr_t)p.v % 16) == 0 &&
-                       (size_t)p.tkv * HD * 2 < (1ull << 31) && (size_t)p.tq * HD * qsz < (1ull << 31);
+                       (size_t)p.kv_rows * HD * 2 < (1ull << 31) && (size_t)p.tq * HD * qsz < (1ull << 31);
     p.dp = !flash ? 0 : HD <= 64 ? 64 : HD <= 128 ? 128 : 256;
     if (!p.dp) return;
     const uint32_t nqt = (p.tq + fa::BQ - 1) / fa::BQ, tiles = p.batch * p.hq * nqt;
-    const uint32_t key_tiles = (p.tkv + fa::BKV - 1) / fa::BKV;
+    const uint32_t key_tiles = (plan_cached(p) + p.tkv + fa::BKV - 1) / fa::BKV;
     const uint32_t min_chunk = std::max<uint32_t>(2, (key_tiles + 63) / 64);
     p.chunk_tiles = std::max<uint32_t>(min_chunk, key_tiles);
     if (tiles >= cus) return;
@@ -848,7 +893,7 @@ void attention_plan(AttnParams& p, uint32_t cus)
             // causal walks start first), chunk by chunk
             uint32_t uq[AttnParams::FA_WG_TAB], uc[AttnParams::FA_WG_TAB], un[AttnParams::FA_WG_TAB], n = 0;
             for (uint32_t qt = nqt; qt-- > 0;)
-                for (uint32_t ch = 0, nc = fa_chunks(p, qt); ch < nc; ++ch, ++n) {
+                for (uint32_t ch = 0, nc = fa_chunks(p, qt, plan_cached(p)); ch < nc; ++ch, ++n) {
                     uq[n] = qt;
                     uc[n] = ch;
                     un[n] = nc;
@@ -868,7 +913,7 @@ void attention_plan(AttnParams& p, uint32_t cus)
 static size_t attention_kv_bytes(const AttnParams& p)
 {
     if (!p.dp || p.kv_dtype != DT_F32) return 0;
-    const size_t n = (size_t)p.batch * p.hkv * p.tkv * p.head_dim;
+    const size_t n = (size_t)p.batch * p.hkv * p.kv_rows * p.head_dim;
     return (2 * n * sizeof(half_t) + 255) & ~(size_t)255;
 }
 
@@ -918,6 +963,13 @@ static hipError_t attention_launch_d(const AttnParams& p, hipStream_t s)
 
 hipError_t attention_launch(const AttnParams& p0, hipStream_t s)
 {
+    if (p0.cache_count && p0.tkv > 0) {
+        const size_t n = (size_t)p0.tkv * p0.head_dim;
+        const uint32_t blocks = (uint32_t)std::min<size_t>((n + 255) / 256, 1024);
+        hipLaunchKernelGGL(attention_append_kernel, dim3(blocks, p0.hkv), dim3(256), 0, s, p0);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     if (!p0.dp) {
         hipLaunchKernelGGL(attention_naive_kernel, dim3(p0.tq, p0.hq, p0.batch), dim3(256), 0, s, p0);
         return hipGetLastError();
@@ -925,7 +977,7 @@ hipError_t attention_launch(const AttnParams& p0, hipStream_t s)
     AttnParams p = p0;
     if (p.kv_dtype == DT_F32) {
         if (!p.ws_kv) return hipErrorInvalidValue;
-        const size_t n = (size_t)p.batch * p.hkv * p.tkv * p.head_dim;
+        const size_t n = (size_t)p.batch * p.hkv * p.kv_rows * p.head_dim;
         half_t* k16 = (half_t*)p.ws_kv;
         half_t* v16 = k16 + n;
         const size_t n4 = n / 4;

@@ -441,16 +441,35 @@ static vai_status make_mask(MaskRule& m, uint32_t tq, uint32_t tkv, uint32_t cau
 
 static vai_status attention_params(const vai_attention_args* a, AttnParams& p)
 {
-    if (!a || !a->q || !a->k || !a->v) return VAI_ERR_INVALID_ARG;
+    if (!a || !a->q) return VAI_ERR_INVALID_ARG;
+    const bool cache = a->cache_size > 0;
+    // K / V: needed unless a cache supplies every key (Tkv = 0)
+    if ((a->tkv > 0 || !cache) && (!a->k || !a->v)) return VAI_ERR_INVALID_ARG;
+    if (cache && (!a->k_cache || !a->v_cache || !a->cache_count)) return VAI_ERR_INVALID_ARG;
     const auto f32_or_f16 = [](int32_t d) { return d == VAI_DTYPE_F32 || d == VAI_DTYPE_F16; };
-    if (!f32_or_f16(a->q_dtype) || !f32_or_f16(a->kv_dtype) || !dtype_ok(a->o_dtype)) return VAI_ERR_DTYPE;
-    if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || a->tkv == 0 || a->head_dim == 0 ||
+    if (!f32_or_f16(a->q_dtype) || !dtype_ok(a->o_dtype)) return VAI_ERR_DTYPE;
+    if (a->tkv > 0 && !f32_or_f16(a->kv_dtype)) return VAI_ERR_DTYPE;
+    if (cache && !f32_or_f16(a->cache_dtype)) return VAI_ERR_DTYPE;
+    if (a->batch == 0 || a->hq == 0 || a->hkv == 0 || a->tq == 0 || (a->tkv == 0 && !cache) || a->head_dim == 0 ||
         a->hq % a->hkv != 0)
         return VAI_ERR_SHAPE;
+    // one counter per call: cached sequences cannot sit at different positions
+    // (attention.h:1016); a ring's tiles must not wrap it; without a ring the
+    // new rows must fit
+    if (cache && (a->batch != 1 || (a->cache_ring && a->cache_size % 64 != 0) ||
+                  (!a->cache_ring && a->tkv > a->cache_size)))
+        return VAI_ERR_SHAPE;
     p = AttnParams{};
-    p.out = a->out; p.q = a->q; p.k = a->k; p.v = a->v;
-    p.o_dtype = a->o_dtype; p.q_dtype = a->q_dtype; p.kv_dtype = a->kv_dtype;
+    p.out = a->out; p.q = a->q;
+    p.o_dtype = a->o_dtype; p.q_dtype = a->q_dtype;
     p.batch = a->batch; p.hq = a->hq; p.hkv = a->hkv; p.tq = a->tq; p.tkv = a->tkv; p.head_dim = a->head_dim;
+    if (cache) {
+        p.k = a->k_cache; p.v = a->v_cache; p.kv_dtype = a->cache_dtype;
+        p.cache_count = a->cache_count; p.kv_rows = a->cache_size; p.ring = a->cache_ring ? 1u : 0u;
+        p.k_new = a->k; p.v_new = a->v; p.new_dtype = a->kv_dtype;
+    } else {
+        p.k = a->k; p.v = a->v; p.kv_dtype = a->kv_dtype; p.kv_rows = a->tkv;
+    }
     p.scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)a->head_dim);
     p.span = a->span;
     if (vai_status st = make_mask(p.mask, a->tq, a->tkv, a->causal, a->span, a->mask_blocks, a->mask_bits,

@@ -73,10 +73,17 @@ struct MaskRule {
         const int64_t e = (int64_t)new_token_end(t) + tkv - tq;
         return e < 0 ? 0 : (e > (int64_t)tkv ? (int64_t)tkv : e);
     }
-    __host__ __device__ int64_t key_start(uint32_t t) const
+    __host__ __device__ int64_t key_start(uint32_t t) const { return key_start_cached(t, 0); }
+    // With a KV cache holding `cached` positions ahead of the tkv new keys
+    // (keys in global positions [0, cached + tkv)): the reference's
+    // kvCacheCount + keyEnd(t) and keyStart(keyPos(t)), keyPos(t) = cached +
+    // max(t + tkv - tq, 0) (/root/reference/vai/shaders/attention-fa.comp:
+    // 137-146, 470-478). cached = 0 is the plain rule.
+    __host__ __device__ int64_t key_end_cached(uint32_t t, uint32_t cached) const { return cached + key_end(t); }
+    __host__ __device__ int64_t key_start_cached(uint32_t t, uint32_t cached) const
     {
         const int64_t pos = (int64_t)t + tkv - tq;
-        const int64_t p = pos < 0 ? 0 : pos;
+        const int64_t p = (int64_t)cached + (pos < 0 ? 0 : pos);
         return (span == 0 || p < (int64_t)span) ? 0 : p + 1 - span;
     }
 };
@@ -158,6 +165,18 @@ struct AttnParams {
     int o_dtype, q_dtype, kv_dtype;
     uint32_t batch, hq, hkv, tq, tkv, head_dim;
     uint32_t dp;                  // flash kernel's padded head dim; 0: the naive kernel
+    // Key rows. Without a cache, k / v hold [batch, hkv, tkv, head_dim] and
+    // kv_rows = tkv. With one (batch 1), k / v are the cache planes [hkv,
+    // kv_rows, head_dim], keys sit in global positions [0, cached + tkv),
+    // position j at row j (ring: j % kv_rows), and cached = *cache_count is
+    // read by the kernels at run time (the reference's kvCacheCount uniform,
+    // which the model rewrites before each forward).
+    const uint32_t* cache_count;  // null: no cache, cached = 0
+    uint32_t kv_rows;
+    uint32_t ring;
+    const void* k_new;            // with a cache: the tkv new rows [hkv, tkv, head_dim] in new_dtype,
+    const void* v_new;            // appended to the cache before the attention reads it
+    int new_dtype;
     float scale;
     uint32_t causal, span;
     MaskRule mask;                // the same rule; blocks > 1 takes the general per-row bounds

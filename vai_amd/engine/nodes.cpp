@@ -371,25 +371,43 @@ void Attention::setCausalMask(const CausalMask& mask)
     if (ownedNet_) ownedNet_->invalidateCommandBuffer();
 }
 
+void Attention::setKvCacheCounter(const uint32_t* counter)
+{
+    require(config_.kvCacheSize > 0, "Attention: a counter needs a KV cache (attention.h:244)");
+    kvCacheCounter_ = counter;
+    if (ownedNet_) ownedNet_->invalidateCommandBuffer();
+}
+
 Attention::Attention(Config config) : config_(config)
 {
     if (config_.numKVHeads == 0) config_.numKVHeads = config_.numQHeads;
     require(config_.numQHeads > 0 && config_.headDim > 0, "Attention: heads and headDim must be positive");
     require(config_.numQHeads % config_.numKVHeads == 0, "Attention: numQHeads must be a multiple of numKVHeads");
-    require(config_.kvCacheSize == 0 && !config_.kvCacheRing, "Attention: the KV cache is not supported");
+    require(config_.kvCacheSize == 0 || config_.kvCacheDtype == Dtype::Fp16 || config_.kvCacheDtype == Dtype::Fp32,
+            "Attention: a KV cache needs kvCacheDtype fp16 or fp32 (attention.h:959)");
+    require(!config_.kvCacheRing || config_.kvCacheSize > 0, "Attention: a ring needs kvCacheSize (attention.h:960)");
+    if (config_.kvCacheRing)
+        config_.kvCacheSize = (config_.kvCacheSize + kvRingAlign - 1) / kvRingAlign * kvRingAlign;
     addSlot("out0", NodeSlot::output);
     addSlot("Q", NodeSlot::input);
     addSlot("K", NodeSlot::input);
     addSlot("V", NodeSlot::input);
     addSlot("partialO", NodeSlot::temporary);
+    if (config_.kvCacheSize > 0) {
+        addSlot("K_cache", NodeSlot::persistent);
+        addSlot("V_cache", NodeSlot::persistent);
+        (*this)["K_cache"] = Tensor({config_.numKVHeads, config_.kvCacheSize, config_.headDim}, config_.kvCacheDtype);
+        (*this)["V_cache"] = Tensor({config_.numKVHeads, config_.kvCacheSize, config_.headDim}, config_.kvCacheDtype);
+    }
 }
 
 vai_attention_args Attention::args(bool withBuffers) const
 {
     vai_attention_args a{};
+    const bool hasKv = tkv_ > 0;
     a.o_dtype = code(outputDtype());
     a.q_dtype = code((*this)["Q"].dtype());
-    a.kv_dtype = code((*this)["K"].dtype());
+    a.kv_dtype = hasKv ? code((*this)["K"].dtype()) : VAI_DTYPE_NONE;
     a.batch = batch_;
     a.hq = config_.numQHeads;
     a.hkv = config_.numKVHeads;
@@ -401,13 +419,29 @@ vai_attention_args Attention::args(bool withBuffers) const
     // the size query needs non-null, 16-byte aligned operands (as the pool's
     // buffers are); their values do not matter
     alignas(16) static char dummy[16];
-    a.q = a.k = a.v = dummy;
+    a.q = dummy;
+    a.k = a.v = hasKv ? dummy : nullptr;
     a.out = dummy;
+    if (config_.kvCacheSize > 0) {
+        a.k_cache = a.v_cache = dummy;
+        a.cache_count = reinterpret_cast<const uint32_t*>(dummy);
+        a.cache_size = config_.kvCacheSize;
+        a.cache_dtype = code(config_.kvCacheDtype);
+        a.cache_ring = config_.kvCacheRing ? 1u : 0u;
+    }
     if (withBuffers) {
         a.out = (*this)["out0"].devicePtr();
         a.q = (*this)["Q"].devicePtr();
-        a.k = (*this)["K"].devicePtr();
-        a.v = (*this)["V"].devicePtr();
+        if (hasKv) {
+            a.k = (*this)["K"].devicePtr();
+            a.v = (*this)["V"].devicePtr();
+        }
+        if (config_.kvCacheSize > 0) {
+            require(kvCacheCounter_ != nullptr, "Attention: a KV cache needs setKvCacheCounter");
+            a.k_cache = (*this)["K_cache"].devicePtr();
+            a.v_cache = (*this)["V_cache"].devicePtr();
+            a.cache_count = kvCacheCounter_;
+        }
         const Tensor& part = (*this)["partialO"];
         a.workspace = part.validShape() ? part.devicePtr() : nullptr;
         a.workspace_bytes = part.validShape() ? part.numBytes() : 0;
@@ -421,17 +455,30 @@ void Attention::prepare()
     const Tensor& k = (*this)["K"];
     const Tensor& v = (*this)["V"];
     const auto& qs = q.shape();
-    const auto& ks = k.shape();
-    require(qs.size() >= 3 && ks.size() == qs.size() && v.shape() == ks, "Attention: Q, K, V must be [..., H, T, D]");
-    require(qs.back() == config_.headDim && ks.back() == config_.headDim, "Attention: headDim mismatch");
-    require(qs[qs.size() - 3] == config_.numQHeads && ks[ks.size() - 3] == config_.numKVHeads,
-            "Attention: head counts mismatch");
-    require(q.dtype() != Dtype::None && k.dtype() != Dtype::None, "Attention: Q, K, V need a dtype");
-    require(v.dtype() == k.dtype(), "Attention: K and V must share a dtype (attention.h:1014)");
+    // without K / V (Tkv = 0) the keys are the cache's alone (attention.h:1001-1004)
+    const bool hasKv = k.validShape();
+    require(hasKv == v.validShape(), "Attention: K and V are wired together");
+    require(hasKv || config_.kvCacheSize > 0, "Attention: K / V unwired without a KV cache");
+    require(qs.size() >= 3 && qs.back() == config_.headDim && qs[qs.size() - 3] == config_.numQHeads,
+            "Attention: Q must be [..., numQHeads, Tq, headDim]");
+    require(q.dtype() != Dtype::None, "Attention: Q needs a dtype");
     batch_ = outerSize(qs, 3);
-    require(outerSize(ks, 3) == batch_, "Attention: Q and K batch axes differ");
     tq_ = qs[qs.size() - 2];
-    tkv_ = ks[ks.size() - 2];
+    tkv_ = 0;
+    if (hasKv) {
+        const auto& ks = k.shape();
+        require(ks.size() == qs.size() && v.shape() == ks, "Attention: Q, K, V must be [..., H, T, D]");
+        require(ks.back() == config_.headDim && ks[ks.size() - 3] == config_.numKVHeads,
+                "Attention: K / V head count or headDim mismatch");
+        require(k.dtype() != Dtype::None && v.dtype() == k.dtype(), "Attention: K and V must share a dtype (attention.h:1014)");
+        require(outerSize(ks, 3) == batch_, "Attention: Q and K batch axes differ");
+        tkv_ = ks[ks.size() - 2];
+    }
+    // one counter per dispatch: one sequence with a cache (attention.h:1016)
+    require(batch_ == 1 || config_.kvCacheSize == 0, "Attention: a KV cache serves one sequence");
+    for (const char* name : {"K_cache", "V_cache"})
+        if (config_.kvCacheSize > 0 && !(*this)[name].gpuBufferBound())
+            (*this)[name].bindBuffer(bufferPool().requestBuffer((*this)[name].numBytes()));
     // token-major [..., Tq, Hq, Dh] (attention.h:1220-1223): leading axes as they came
     std::vector<uint32_t> os = qs;
     os[os.size() - 3] = tq_;

@@ -174,14 +174,20 @@ private:
     CausalMask mask_;
 };
 
-// The reference's Attention node without a KV cache (/root/reference/vai/
-// nodes/attention.h:77-129, 216-240, 979-1304): out0 = softmax(Q K^T /
-// sqrt(headDim) + mask) V per head. Q [..., numQHeads, Tq, headDim] fp32 or
-// fp16, K / V [..., numKVHeads, Tkv, headDim] in their own dtype (fp32 or
-// fp16), out0 token-major [..., Tq, numQHeads, headDim] in the node's output
-// dtype. Queries and keys align at their ends. No mask until setCausalMask
-// is called: every query attends every key. Any head dim. The KV cache
-// (kvCacheSize > 0) is not part of this build: the constructor rejects it.
+// The reference's Attention node (/root/reference/vai/nodes/attention.h:
+// 77-140, 216-245, 959-1304): out0 = softmax(Q K^T / sqrt(headDim) + mask) V
+// per head. Q [..., numQHeads, Tq, headDim] fp32 or fp16, K / V [...,
+// numKVHeads, Tkv, headDim] in their own dtype (fp32 or fp16), out0
+// token-major [..., Tq, numQHeads, headDim] in the node's output dtype.
+// Queries and keys align at their ends. No mask until setCausalMask is
+// called: every query attends every key. Any head dim.
+// kvCacheSize > 0 adds the KV cache: the persistent slots "K_cache" /
+// "V_cache" [numKVHeads, kvCacheSize, headDim] in kvCacheDtype (a ring rounds
+// its size up to kvRingAlign) and a counter the model owns and rewrites
+// before each forward (setKvCacheCounter: a device-readable uint32, read when
+// the kernels run, so a recorded forward follows it). Each forward appends
+// its Tkv new K / V rows after the cached ones and attends both; K / V may
+// stay unwired (Tkv = 0) to attend the cache alone. One sequence only.
 // "partialO" holds the workspace (fp16 K / V copies, key-split partials)
 // when a launch needs one.
 class Attention : public Node
@@ -191,10 +197,11 @@ public:
         uint32_t headDim;
         uint32_t numQHeads;
         uint32_t numKVHeads = 0;              // for GQA (Hkv < numQHeads); 0: numQHeads
-        uint32_t kvCacheSize = 0;             // must be 0 here: no cache
-        Dtype kvCacheDtype = Dtype::None;
-        bool kvCacheRing = false;
+        uint32_t kvCacheSize = 0;             // tokens the cache holds; 0: no cache at all
+        Dtype kvCacheDtype = Dtype::None;     // required with a cache
+        bool kvCacheRing = false;             // keep the last kvCacheSize positions (rounded up to kvRingAlign)
     } config_;
+    static constexpr uint32_t kvRingAlign = 256;
 
     explicit Attention(Config config);
     void prepare() override;
@@ -205,9 +212,13 @@ public:
     // reference rewrites a uniform buffer without re-recording; here the mask
     // is part of the recorded launch, so the next forward re-records.
     void setCausalMask(const CausalMask& mask);
+    // The positions the cache holds (attention.h:242-246): a device-readable
+    // uint32 the model writes before each forward; the node never writes it.
+    void setKvCacheCounter(const uint32_t* counter);
 
 private:
     vai_attention_args args(bool withBuffers) const;
+    const uint32_t* kvCacheCounter_ = nullptr;
     uint32_t batch_ = 1, tq_ = 0, tkv_ = 0;
     CausalMask mask_;
 };

@@ -208,11 +208,21 @@ PYBIND11_MODULE(_pyvai, m)
                  n.setCausalMask(node::CausalMask::make(bits, block_ends(ends), span));
              }, py::arg("bits"), py::arg("block_end") = std::vector<uint32_t>{}, py::arg("span") = 0);
     py::class_<node::Attention, Node>(nodes, "AttentionNode")
-        .def(py::init([](uint32_t num_q_heads, uint32_t head_dim, uint32_t num_kv_heads) {
-                 node::Attention::Config c{.headDim = head_dim, .numQHeads = num_q_heads, .numKVHeads = num_kv_heads};
+        .def(py::init([](uint32_t num_q_heads, uint32_t head_dim, uint32_t num_kv_heads, uint32_t kv_cache_size,
+                         py::object kv_cache_dtype, bool kv_cache_ring) {
+                 node::Attention::Config c{.headDim = head_dim, .numQHeads = num_q_heads, .numKVHeads = num_kv_heads,
+                                           .kvCacheSize = kv_cache_size,
+                                           .kvCacheDtype = kv_cache_dtype.is_none() ? Dtype::None
+                                                                                    : kv_cache_dtype.cast<Dtype>(),
+                                           .kvCacheRing = kv_cache_ring};
                  return std::make_unique<node::Attention>(c);
              }),
-             py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0)
+             py::arg("num_q_heads"), py::arg("head_dim"), py::arg("num_kv_heads") = 0, py::arg("kv_cache_size") = 0,
+             py::arg("kv_cache_dtype") = py::none(), py::arg("kv_cache_ring") = false)
+        .def("set_kv_cache_counter", [](node::Attention& n, uintptr_t ptr) {
+                 n.setKvCacheCounter(reinterpret_cast<const uint32_t*>(ptr));
+             }, py::arg("device_ptr"))
+        .def_property_readonly("kv_cache_size", [](node::Attention& n) { return n.config_.kvCacheSize; })
         .def("set_causal_mask", [](node::Attention& n, uint32_t bits, std::vector<uint32_t> ends, uint32_t span) {
                  n.setCausalMask(node::CausalMask::make(bits, block_ends(ends), span));
              }, py::arg("bits"), py::arg("block_end") = std::vector<uint32_t>{}, py::arg("span") = 0);

@@ -236,7 +236,7 @@ def build_cases(capi, stream, which):
         fn5.keep = [wt, bias, x, out, a5, ws5]
         flops = 2 * 6400 * 128 * 1152
         cases["5"] = Case("YOLOX-s 3x3 conv in[1,128,80,80] W[128,128,3,3] fp16 +bias SiLU, fp32 out",
-                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn5, "conv3_pipe_kernel<5,4> (implicit GEMM, NCHW rows transposed by the LDS read, packed weight; 4 waves x 16 output channels x one row over all 4 channel blocks, block-pipelined copies)", flops, 5210368, "f16", "5")
+                          "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fn5, "conv3_pipe_kernel<5,4,4> (implicit GEMM, NCHW rows transposed by the LDS read, packed weight; 4 waves x 16 output channels x one row over all 4 channel blocks, block-pipelined copies, SiLU epilogue stored per fragment during the last block)", flops, 5210368, "f16", "5")
     for key, (ci, co, ks, st, hw) in {"5/k1s1": (256, 128, 1, 1, 40), "5/k3s2": (128, 256, 3, 2, 80)}.items():
         if key not in which:
             continue

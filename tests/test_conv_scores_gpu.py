@@ -219,6 +219,36 @@ def test_conv3_output_alignment(gpu, off):
     assert_close(out.numpy(), oracle.conv2d(x, w, b, None, r, epi="SILU", order=0), FP16)
 
 
+@pytest.mark.parametrize("epi, odt, scaled", [
+    ("NONE", np.float16, False), ("RELU", np.float16, True), ("SILU", np.float16, False),
+    ("SIGMOID", np.float32, True), ("SILU", np.float32, True), ("NONE", np.float32, False),
+])
+def test_conv3_cheap_epilogue(gpu, epi, odt, scaled):
+    """The 3x3 plan's branch-free epilogue (none / SiLU, no residual), whose
+    fragments are stored during the last channel block, beside the general
+    one (ReLU, sigmoid): both output dtypes, a scale, an output-channel tail
+    (80 = 64 + 16: the second workgroup's waves past Co store nothing), and
+    nothing written past the output (a guard band after it keeps its fill)."""
+    rng = np.random.default_rng(17)
+    ci, co, hi, wi, batch = 64, 80, 12, 48, 2
+    w = draw(normal((co, ci, 3, 3), 1.0 / np.sqrt(ci * 9)), rng, np.float16)
+    b = draw(normal((co,), 0.1), rng, np.float16)
+    s = draw(uniform((co,), 0.5, 1.5), rng, np.float16) if scaled else None
+    x = draw((batch, ci, hi, wi), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    shape = (batch, co, hi, wi)
+    nbytes = int(np.prod(shape)) * np.dtype(odt).itemsize
+    fill = np.full(nbytes + 4096, 0xAB, np.uint8)
+    out = _Offset(gpu, shape, odt, 0, None)
+    out._base = D(fill)
+    out.ptr = out._base.ptr
+    print(f"conv3 cheap epilogue {epi} {np.dtype(odt).name} scaled={scaled}", flush=True)
+    gpu.conv2d(out, D(x), D(w), D(b), D(s) if scaled else None, None, epi=epi)
+    got = out.numpy().astype(np.float32)
+    assert_close(got, oracle.conv2d(x, w, b, s, epi=epi), FP16)
+    assert (out._base.numpy()[nbytes:] == 0xAB).all()
+
+
 def run_scores(capi, q, k, **kw):
     dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
     out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)

@@ -709,7 +709,57 @@ __device__ __forceinline__ void conv3_taps_store(const ConvParams& p, float4v (&
     }
 }
 
-template <int NF, int NB>
+// The common epilogues (none, SiLU; no residual) as a kernel parameter and
+// without a branch: the output dtype picks one of two buffer resources, the
+// other holding no bytes (its store is dropped by the range check), as is a
+// lane past Co. With no branch in it, one fragment's output can be stored in
+// the middle of the last block's MFMA steps without the control flow that
+// would make the compiler's waits conservative around it. (A runtime choice
+// of the activation, as a select or as bit masks, cost 0.2-1 us at config 5.)
+typedef uint32_t cv_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t cv_u32x2 __attribute__((ext_vector_type(2)));
+struct Conv3CheapOut {
+    __amdgpu_buffer_rsrc_t o32, o16;
+    // element index of the lane's first output of fragment 0, 2^28 for a
+    // lane past Co: its byte offsets (2^30 fp32, 2^29 fp16) then lie past
+    // either resource's range, which the plan keeps under 2^30 bytes
+    uint32_t o;
+    float bias, sc;
+};
+
+template <int NF, int F, int EPI>
+__device__ __forceinline__ void conv3_tap_frag_cheap(const Conv3CheapOut& c, float4v (&P)[3][NF], int fg, int lane)
+{
+    constexpr int f = F;
+    const int src_lo = ((lane + 48) & 63) * 4, src_hi = ((lane + 16) & 63) * 4;
+    const float off0 = fg == 3 ? (f > 0 ? P[0][f > 0 ? f - 1 : 0][3] : 0.f) : P[0][f][3];
+    const float off2 = fg == 0 ? (f + 1 < NF ? P[2][f + 1 < NF ? f + 1 : f][0] : 0.f) : P[2][f][0];
+    const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lo, __builtin_bit_cast(int, off0)));
+    const float x2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_hi, __builtin_bit_cast(int, off2)));
+    float4v acc;
+    acc[0] = P[1][f][0] + x0 + P[2][f][1];
+    acc[1] = P[1][f][1] + P[0][f][0] + P[2][f][2];
+    acc[2] = P[1][f][2] + P[0][f][1] + P[2][f][3];
+    acc[3] = P[1][f][3] + P[0][f][2] + x2;
+    float4v v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = cv_act<EPI>(fmaf(acc[r], c.sc, c.bias));
+    const uint32_t e = c.o + 16 * f;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(cv_u32x4, v), c.o32, (int)(e * 4), 0, 0);
+    const half4 h = __builtin_convertvector(v, half4);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(cv_u32x2, h), c.o16, (int)(e * 2), 0, 0);
+}
+
+// The epilogue kind of the cheap form (-1: the general epilogue); the
+// output's byte offsets then also fit the buffer resources' 31 bits.
+static int conv3_cheap_kind(const ConvParams& p)
+{
+    const int k = p.epilogue;
+    const bool fits = (size_t)p.batch * p.co * p.ho * p.wo * 4 < (1ull << 30);
+    return !p.residual && fits && (k == 0 || k == 4) ? k : -1;
+}
+
+template <int NF, int NB, int EK>
 __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
 {
     using G = cvp::Geo<NF>;
@@ -779,6 +829,17 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
     for (int k = 0; k < 3; ++k)
 #pragma unroll
         for (int f = 0; f < NF; ++f) P[k][f] = (float4v)0.f;
+    constexpr bool CHEAP = EK >= 0;   // the cheap epilogue, activation EK
+    Conv3CheapOut cheap;
+    if constexpr (CHEAP) {
+        const uint32_t bytes = p.batch * p.co * p.ho * p.wo * 4;
+        const bool o16 = p.o_dtype == DT_F16;
+        cheap.o32 = __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, o16 ? 0 : (int)bytes, 0x00020000);
+        cheap.o16 = __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, o16 ? (int)(bytes / 2) : 0, 0x00020000);
+        cheap.o = co < p.co ? ((b * p.co + co) * p.ho + ho) * p.wo + 4 * fg : 0x10000000u;
+        cheap.bias = bias;
+        cheap.sc = sc;
+    }
     // B source lane (k, q) = (fr / 4, fr % 4) of group fg: channel 8 fg + k of
     // the block, columns 4 q ..; the high half 4 channels on
     const uint32_t lbase =
@@ -820,22 +881,41 @@ __global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
                     });
                 __builtin_amdgcn_sched_barrier(0);
             }
+            // cheap epilogue: in the last block, fragment f's taps are all
+            // issued at step 2 NF + f, and fragment f - 1 then has every
+            // value it needs; its stores leave while the MFMAs go on
+            if constexpr (CHEAP && j + 1 == NB && kh == 2 && f > 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                conv3_tap_frag_cheap<NF, (f > 0 ? f - 1 : 0), (EK >= 0 ? EK : 0)>(cheap, P, fg, lane);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         });
         __builtin_amdgcn_sched_barrier(0);
     });
 
-    conv3_taps_store<NF>(p, P, bias, sc, co, ho, b, fg, lane);
+    if constexpr (CHEAP) conv3_tap_frag_cheap<NF, NF - 1, (EK >= 0 ? EK : 0)>(cheap, P, fg, lane);
+    else conv3_taps_store<NF>(p, P, bias, sc, co, ho, b, fg, lane);
+}
+
+template <int NF, int NB, int EK>
+static hipError_t launch_pipe_form(const ConvParams& p, hipStream_t s)
+{
+    constexpr uint32_t lds = NB * cvp::Geo<NF>::CBB;
+    static PerDevice lds_once;
+    hipError_t e = set_max_lds(lds_once, (const void*)conv3_pipe_kernel<NF, NB, EK>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((conv3_pipe_kernel<NF, NB, EK>), dim3((p.co + 63) / 64, p.ho, p.batch), dim3(256), lds, s, p);
+    return hipGetLastError();
 }
 
 template <int NF, int NB>
 static hipError_t launch_pipe(const ConvParams& p, hipStream_t s)
 {
-    constexpr uint32_t lds = NB * cvp::Geo<NF>::CBB;
-    static PerDevice lds_once;
-    hipError_t e = set_max_lds(lds_once, (const void*)conv3_pipe_kernel<NF, NB>, lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((conv3_pipe_kernel<NF, NB>), dim3((p.co + 63) / 64, p.ho, p.batch), dim3(256), lds, s, p);
-    return hipGetLastError();
+    switch (conv3_cheap_kind(p)) {
+    case 0: return launch_pipe_form<NF, NB, 0>(p, s);
+    case 4: return launch_pipe_form<NF, NB, 4>(p, s);
+    default: return launch_pipe_form<NF, NB, -1>(p, s);
+    }
 }
 
 template <int NF>

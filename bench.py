@@ -259,7 +259,7 @@ def build_cases(capi, stream, which):
         byts = ci * hw * hw * 2 + co * ci * ks * ks * 2 + co * 2 + co * ho * ho * 4
         cases[key] = Case(f"YOLOX-s {ks}x{ks}/s{st} conv in[1,{ci},{hw},{hw}] W[{co},{ci},{ks},{ks}] fp16 +bias SiLU, fp32 out",
                           "TFLOP/s", flops / 1e12, "mfma", FP16_PEAK_TFLOPS, fnc,
-                          "conv1_pipe_kernel<8> (pointwise: 16 flat positions x 64 output channels per workgroup)" if ks == 1
+                          "conv1_pipe_kernel<8,4> (pointwise: 16 flat positions x 64 output channels per workgroup, branch-free SiLU epilogue, one 16-byte store per lane)" if ks == 1
                           else f"conv_kernel<{ks}> (implicit GEMM, packed weight)",
                           flops, byts, "f16", key)
     if "read" in which or "empty" in which or "write" in which:

@@ -249,6 +249,32 @@ def test_conv3_cheap_epilogue(gpu, epi, odt, scaled):
     assert (out._base.numpy()[nbytes:] == 0xAB).all()
 
 
+@pytest.mark.parametrize("epi, odt, scaled", [("NONE", np.float16, True), ("SILU", np.float32, False),
+                                             ("SILU", np.float16, True), ("RELU", np.float32, False)])
+def test_conv1_cheap_epilogue(gpu, epi, odt, scaled):
+    """The pointwise plan's branch-free epilogue (none / SiLU, no residual;
+    ReLU takes the general one): four consecutive positions per store, an
+    output-channel tail (80), 120 positions (the last workgroup's second half
+    lies past H W), batch 2, and a guard band after the output that keeps
+    its fill."""
+    rng = np.random.default_rng(23)
+    ci, co, h, w_, batch = 48, 80, 10, 12, 2
+    w = draw(normal((co, ci, 1, 1), 1.0 / np.sqrt(ci)), rng, np.float16)
+    b = draw(normal((co,), 0.1), rng, np.float16)
+    s = draw(uniform((co,), 0.5, 1.5), rng, np.float16) if scaled else None
+    x = draw((batch, ci, h, w_), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    shape = (batch, co, h, w_)
+    nbytes = int(np.prod(shape)) * np.dtype(odt).itemsize
+    out = _Offset(gpu, shape, odt, 0, None)
+    out._base = D(np.full(nbytes + 4096, 0xAB, np.uint8))
+    out.ptr = out._base.ptr
+    print(f"conv1 cheap epilogue {epi} {np.dtype(odt).name} scaled={scaled}", flush=True)
+    gpu.conv2d(out, D(x), D(w), D(b), D(s) if scaled else None, None, epi=epi)
+    assert_close(out.numpy().astype(np.float32), oracle.conv2d(x, w, b, s, epi=epi), FP16)
+    assert (out._base.numpy()[nbytes:] == 0xAB).all()
+
+
 def run_scores(capi, q, k, **kw):
     dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
     out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)

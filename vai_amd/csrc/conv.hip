@@ -752,7 +752,7 @@ __device__ __forceinline__ void conv3_tap_frag_cheap(const Conv3CheapOut& c, flo
 
 // The epilogue kind of the cheap form (-1: the general epilogue); the
 // output's byte offsets then also fit the buffer resources' 31 bits.
-static int conv3_cheap_kind(const ConvParams& p)
+static int conv_cheap_kind(const ConvParams& p)
 {
     const int k = p.epilogue;
     const bool fits = (size_t)p.batch * p.co * p.ho * p.wo * 4 < (1ull << 30);
@@ -911,7 +911,7 @@ static hipError_t launch_pipe_form(const ConvParams& p, hipStream_t s)
 template <int NF, int NB>
 static hipError_t launch_pipe(const ConvParams& p, hipStream_t s)
 {
-    switch (conv3_cheap_kind(p)) {
+    switch (conv_cheap_kind(p)) {
     case 0: return launch_pipe_form<NF, NB, 0>(p, s);
     case 4: return launch_pipe_form<NF, NB, 4>(p, s);
     default: return launch_pipe_form<NF, NB, -1>(p, s);
@@ -941,7 +941,9 @@ static hipError_t launch_pipe_nb(const ConvParams& p, hipStream_t s)
 // work per workgroup is a few MFMAs, so the time is the load latency. YOLOX's
 // CSP pointwise conv ([1,256,40,40] -> 128, 200 workgroups): 3.15-3.26 us
 // against 4.46 with the general kernel; 32 positions per workgroup 4.43, 32
-// output channels per workgroup 3.33-3.34, 16 channels 3.71.
+// output channels per workgroup 3.33-3.34, 16 channels 3.71. With the cheap
+// epilogue (no residual, none / SiLU) 2.45 us: one 16-byte store per lane
+// and no branch instead of four 4-byte stores behind per-channel checks.
 template <int EPI, bool O16>
 __device__ __forceinline__ void conv1_store(const ConvParams& p, const float4v& acc, uint32_t co_lane, uint32_t pos,
                                             uint32_t b)
@@ -967,7 +969,10 @@ __device__ __forceinline__ void conv1_store(const ConvParams& p, const float4v& 
     }
 }
 
-template <int NB>
+// EK >= 0: the cheap epilogue with activation EK (see Conv3CheapOut). The
+// MFMA then takes the input as A and the weight as B, so that a lane holds
+// one output channel at four consecutive positions: one 16-byte store.
+template <int NB, int EK>
 __global__ __launch_bounds__(256) void conv1_pipe_kernel(ConvParams p)
 {
     extern __shared__ half8 smem[];
@@ -985,6 +990,16 @@ __global__ __launch_bounds__(256) void conv1_pipe_kernel(ConvParams p)
     half8 wa[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) wa[j] = *(const half8*)(p.wp + (((size_t)oblk * NB + j) * 64 + lane) * 8);
+    // the cheap epilogue's bias and scale of the lane's channel, loaded with
+    // the rest (a missing one reads the packed weight and is ignored)
+    float bias = 0.f, sc = 1.f;
+    if constexpr (EK >= 0) {
+        const uint32_t cc = min(co0 + wave * 16 + fr, p.co - 1);
+        const float bv = (float)(p.bias ? (const half_t*)p.bias : p.wp)[cc];
+        const float sv = (float)(p.scale ? (const half_t*)p.scale : p.wp)[cc];
+        bias = p.bias ? bv : 0.f;
+        sc = p.scale ? sv : 1.f;
+    }
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)uniform_ptr((const half_t*)p.x + (size_t)b * p.ci * HW), (short)0, (int)(p.ci * HW * 2), 0x00020000);
 #pragma unroll
@@ -1006,8 +1021,28 @@ __global__ __launch_bounds__(256) void conv1_pipe_kernel(ConvParams p)
     for (int j = 0; j < NB; ++j) {
         const half4 lo = cv_read_tr16(base + j * 1024);
         const half4 hi = cv_read_tr16(base + j * 1024 + 4 * 32);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[j], __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
-                                                     acc, 0, 0, 0);
+        const half8 xv = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        if constexpr (EK >= 0) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wa[j], acc, 0, 0, 0);
+        else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[j], xv, acc, 0, 0, 0);
+    }
+    if constexpr (EK >= 0) {
+        // D[pos][co]: lane (fr, fg) holds channel co0 + 16 wave + fr at
+        // positions p0 + 4 fg .. +3 (H W % 8 == 0: all four or none inside)
+        const uint32_t co = co0 + wave * 16 + fr, q = p0 + 4 * fg;
+        const uint32_t bytes = p.batch * p.co * HW * 4;
+        const bool o16 = p.o_dtype == DT_F16;
+        const uint32_t e = co < p.co && q < HW ? (b * p.co + co) * HW + q : 0x10000000u;
+        float4v v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = cv_act<(EK >= 0 ? EK : 0)>(fmaf(acc[r], sc, bias));
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(cv_u32x4, v),
+            __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, o16 ? 0 : (int)bytes, 0x00020000), (int)(e * 4), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(
+            __builtin_bit_cast(cv_u32x2, __builtin_convertvector(v, half4)),
+            __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, o16 ? (int)(bytes / 2) : 0, 0x00020000), (int)(e * 2), 0,
+            0);
+        return;
     }
     // D[i][j] of the 16x16 fragment: lane j + 16 (i / 4), register i % 4
     const uint32_t co_lane = co0 + wave * 16 + fg * 4, pos = p0 + fr;
@@ -1031,13 +1066,23 @@ static bool conv1_pipe_ok(const ConvParams& p, int x_dt)
            (size_t)p.ci * HW * 2 < (1ull << 31);
 }
 
+template <int NB, int EK>
+static hipError_t launch_conv1_form(const ConvParams& p, hipStream_t s)
+{
+    const uint32_t HW = p.ho * p.wo;
+    hipLaunchKernelGGL((conv1_pipe_kernel<NB, EK>), dim3((HW + 15) / 16, (p.co + 63) / 64, p.batch), dim3(256),
+                       NB * 1024, s, p);
+    return hipGetLastError();
+}
+
 template <int NB>
 static hipError_t launch_conv1(const ConvParams& p, hipStream_t s)
 {
-    const uint32_t HW = p.ho * p.wo;
-    hipLaunchKernelGGL(conv1_pipe_kernel<NB>, dim3((HW + 15) / 16, (p.co + 63) / 64, p.batch), dim3(256), NB * 1024, s,
-                       p);
-    return hipGetLastError();
+    switch (conv_cheap_kind(p)) {
+    case 0: return launch_conv1_form<NB, 0>(p, s);
+    case 4: return launch_conv1_form<NB, 4>(p, s);
+    default: return launch_conv1_form<NB, -1>(p, s);
+    }
 }
 
 static hipError_t launch_conv1_nb(const ConvParams& p, hipStream_t s)

@@ -85,6 +85,59 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(half_t* __restrict__ d
     }
 }
 
+// The activation of epilogue kind EPI (the same formulas as epilogue()).
+template <int EPI>
+__device__ __forceinline__ float cv_act(float x)
+{
+    if constexpr (EPI == 1) return x > 0.f ? x : 0.f;
+    else if constexpr (EPI == 2) return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
+    else if constexpr (EPI == 3) return 0.5f * x * (1.0f + fast_tanh(0.79788456080286535f * (x + 0.044715f * x * x * x)));
+    else if constexpr (EPI == 4) return x * fast_rcp(1.0f + fast_exp(-x));
+    else if constexpr (EPI == 5) return fast_rcp(1.0f + fast_exp(-x));
+    else return x;
+}
+
+// conv_store's 16-byte form: 4 consecutive positions of one output channel
+// per work item, four 16-byte partial-sum reads and one 16-byte (fp32) or
+// 8-byte (fp16) store. A row of Wo outputs stays 16-byte aligned (Ho Wo and
+// Wo are multiples of 4). The activation, the residual and the output dtype
+// are template parameters: chosen per element at run time they left a
+// branch in every output.
+template <int CT, int EPI, bool RES, bool O16>
+__device__ __forceinline__ void conv_store_vec4(const ConvParams& p, const float* red, uint32_t rw, const float* epi_bs,
+                                                uint32_t co0, uint32_t ho, uint32_t b)
+{
+    constexpr int NT = CT / 4 * 64;
+    const size_t HoWo = (size_t)p.ho * p.wo;
+    const bool before = p.residual_order == 1;
+    const uint32_t q4 = p.wo / 4, items = CT * q4;
+    for (uint32_t it = threadIdx.x; it < items; it += NT) {
+        const uint32_t col = it / q4, wo = (it % q4) * 4, co = co0 + col;
+        if (co >= p.co) continue;
+        float4v v = *(const float4v*)(red + (size_t)col * rw + wo);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CT + col) * rw + wo);
+        const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CT + col] : 1.f;
+        const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
+        float4v rr = (float4v)0.f;
+        if constexpr (RES) {
+            if (p.residual_dtype == DT_F16) rr = __builtin_convertvector(*(const half4*)((const half_t*)p.residual + o), float4v);
+            else rr = *(const float4v*)((const float*)p.residual + o);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // (sc is 1 without a scale: fma(a, 1, b) is exactly a + b)
+            float x = fmaf(v[e], sc, bias);
+            if constexpr (RES) x += before ? rr[e] : 0.f;
+            x = cv_act<EPI>(x);
+            if constexpr (RES) x += before ? 0.f : rr[e];
+            v[e] = x;
+        }
+        if constexpr (O16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(v, half4);
+        else *(float4v*)((float*)p.out + o) = v;
+    }
+}
+
 // Scale, bias, residual and activation of a workgroup's CT output channels
 // x one output row, from the partial sums of its four channel-block waves in
 // LDS (red[w][CT][rw], positions along a row), with stores per output row.
@@ -100,34 +153,23 @@ __device__ __forceinline__ void conv_store(const ConvParams& p, const float* red
     const size_t HoWo = (size_t)p.ho * p.wo;
     const bool vec4 = p.wo % 4 == 0 && (uintptr_t)p.out % 16 == 0 && (uintptr_t)p.residual % 16 == 0;
     if (vec4) {
-        // 4 consecutive positions of one output channel per work item: four
-        // 16-byte partial-sum reads, one 16-byte (fp32) or 8-byte (fp16)
-        // store. A row of Wo outputs stays 16-byte aligned (Ho Wo and Wo
-        // are multiples of 4).
-        const uint32_t q4 = p.wo / 4, items = CT * q4;
-        for (uint32_t it = tid; it < items; it += NT) {
-            const uint32_t col = it / q4, wo = (it % q4) * 4, co = co0 + col;
-            if (co >= p.co) continue;
-            float4v v = *(const float4v*)(red + (size_t)col * rw + wo);
-#pragma unroll
-            for (int w = 1; w < 4; ++w) v += *(const float4v*)(red + ((size_t)w * CT + col) * rw + wo);
-            const float bias = p.bias ? epi_bs[col] : 0.f, sc = p.scale ? epi_bs[CT + col] : 1.f;
-            const size_t o = ((size_t)b * p.co + co) * HoWo + (size_t)ho * p.wo + wo;
-            float4v rr = (float4v)0.f;
-            if (p.residual) {
-                if (p.residual_dtype == DT_F16) rr = __builtin_convertvector(*(const half4*)((const half_t*)p.residual + o), float4v);
-                else rr = *(const float4v*)((const float*)p.residual + o);
+        const bool res = p.residual != nullptr, o16 = p.o_dtype == DT_F16;
+        auto go = [&](auto E) __attribute__((always_inline)) {
+            if (res) {
+                if (o16) conv_store_vec4<CT, E, true, true>(p, red, rw, epi_bs, co0, ho, b);
+                else conv_store_vec4<CT, E, true, false>(p, red, rw, epi_bs, co0, ho, b);
+            } else {
+                if (o16) conv_store_vec4<CT, E, false, true>(p, red, rw, epi_bs, co0, ho, b);
+                else conv_store_vec4<CT, E, false, false>(p, red, rw, epi_bs, co0, ho, b);
             }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float x = p.scale ? fmaf(v[e], sc, bias) : v[e] + bias;
-                if (p.residual && p.residual_order == 1) x += rr[e];
-                x = epilogue(x, p.epilogue);
-                if (p.residual && p.residual_order == 0) x += rr[e];
-                v[e] = x;
-            }
-            if (p.o_dtype == DT_F16) *(half4*)((half_t*)p.out + o) = __builtin_convertvector(v, half4);
-            else *(float4v*)((float*)p.out + o) = v;
+        };
+        switch (p.epilogue) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 3: go(std::integral_constant<int, 3>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        case 5: go(std::integral_constant<int, 5>{}); break;
+        default: go(std::integral_constant<int, 0>{}); break;
         }
         return;
     }
@@ -410,17 +452,6 @@ __device__ __forceinline__ float cv_row_ror(float x)
 // (32 x 2 NF items, one pass): the residual loads first, then the four
 // partial sums from LDS, scale and bias, the activation chosen once per
 // thread (EPI), and one 32-byte (fp32) or 16-byte (fp16) store.
-template <int EPI>
-__device__ __forceinline__ float cv_act(float x)
-{
-    if constexpr (EPI == 1) return x > 0.f ? x : 0.f;
-    else if constexpr (EPI == 2) return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
-    else if constexpr (EPI == 3) return 0.5f * x * (1.0f + fast_tanh(0.79788456080286535f * (x + 0.044715f * x * x * x)));
-    else if constexpr (EPI == 4) return x * fast_rcp(1.0f + fast_exp(-x));
-    else if constexpr (EPI == 5) return fast_rcp(1.0f + fast_exp(-x));
-    else return x;
-}
-
 template <int EPI>
 __device__ __forceinline__ void cv_finish8(float8v& v, const float8v& rr, bool res, uint32_t order, float sc, float bias,
                                            bool scaled)

@@ -284,7 +284,10 @@ __global__ __launch_bounds__(256, T == 128 ? 2 : (TRI ? 5 : 4)) void scores_kern
 // us with the hidden tiles' 16-byte stores and 7.0-7.2 us with the computed
 // tiles' 4-byte stores, against 6.4 us for 32 MiB written in contiguous 16 KB
 // runs per wave: the rest of this kernel's time is the longest strips' Q and K
-// loads ahead of their stores.
+// loads ahead of their stores. Units of at most 3 computed tiles with the
+// hidden tiles in units of their own (no loads): 11.1-11.3 against 10.85-11.0
+// us; at most 4 computed tiles so, 11.6: a hidden tile is cheapest as the
+// store a computing unit issues while its first Q and K tiles load.
 template <int D>
 __global__ __launch_bounds__(256, 2) void scores_strip_kernel(GemmParams p)
 {

@@ -206,6 +206,33 @@ def test_attention_kv_cache(gpu, d, hq, hkv, tq, tkv, count, size, ring, causal,
     assert int(cnt.numpy()[0]) == count   # the caller advances the count
 
 
+@pytest.mark.parametrize("d, tq, count, size, ring, blocks, span", [
+    (128, 96, 200, 512, False, (0b101, [24, 72]), 0),    # causal / full (an image) / causal chunk after cached text
+    (64, 40, 300, 256, True, (0b01, [16]), 128),         # a full prefix block in a ring, sliding window
+    (256, 1, 500, 512, False, (0b10, [1]), 0),           # decode step whose block list has one entry
+])
+def test_attention_kv_cache_block_mask(gpu, d, tq, count, size, ring, blocks, span):
+    """The block masks of common/causal_mask.h over a cached chunk: blocks
+    index the call's new tokens (keyEnd = count + newTokenEnd(t) + Tkv -
+    Tq), the cached positions stay visible to every query, and the window
+    counts global positions."""
+    rng = np.random.default_rng(count + tq + d)
+    hq, hkv = 4, 2
+    kc, vc = _cache_planes(rng, hkv, size, d, count, ring, np.float16)
+    q = draw((1, hq, tq, d), rng, np.float16)
+    k = draw((1, hkv, tq, d), rng, np.float16)
+    v = draw((1, hkv, tq, d), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    dkc, dvc = D(kc), D(vc)
+    out = gpu.DeviceArray((1, tq, hq, d), np.float32)
+    print(f"kv cache blocks={blocks} d={d} tq={tq} count={count} size={size} ring={ring} span={span}", flush=True)
+    got = gpu.attention(out, D(q), D(k), D(v), blocks=blocks, span=span,
+                        cache=(dkc, dvc, D(np.array([count], np.uint32)), ring)).numpy()
+    want, wkc, _ = oracle.attention_cached(q[0], k, v, kc, vc, count, ring=ring, span=span, blocks=blocks)
+    assert_close(got[0], want, FP16)
+    np.testing.assert_array_equal(dkc.numpy(), wkc)
+
+
 def test_attention_kv_cache_decode_steps(gpu):
     """Decode as a model runs it: one token per call, the count advanced on
     the device between calls; each step matches the reference's formulas over

@@ -275,6 +275,22 @@ def test_conv1_cheap_epilogue(gpu, epi, odt, scaled):
     assert (out._base.numpy()[nbytes:] == 0xAB).all()
 
 
+@pytest.mark.parametrize("ks, odt", [(1, np.float32), (1, np.float16), (3, np.float16)])
+def test_conv_cheap_epilogue_unaligned_output(gpu, ks, odt):
+    """An output 4 bytes off a 16-byte boundary leaves the cheap epilogue
+    (16- and 8-byte stores) for the general one; the result is the oracle's."""
+    rng = np.random.default_rng(29 + ks)
+    ci, co, hw = 32, 48, 16
+    w = draw(normal((co, ci, ks, ks), 0.1), rng, np.float16)
+    b = draw((co,), rng, np.float16)
+    x = draw((1, ci, hw, hw), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    out = _Offset(gpu, (1, co, hw, hw), odt, 4)
+    print(f"conv k{ks} cheap epilogue, output 4 bytes off, {np.dtype(odt).name}", flush=True)
+    gpu.conv2d(out, D(x), D(w), D(b), None, None, epi="SILU")
+    assert_close(out.numpy().astype(np.float32), oracle.conv2d(x, w, b, epi="SILU"), FP16)
+
+
 def run_scores(capi, q, k, **kw):
     dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
     out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)

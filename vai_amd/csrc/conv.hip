@@ -781,13 +781,14 @@ __device__ __forceinline__ void conv3_tap_frag_cheap(const Conv3CheapOut& c, flo
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(cv_u32x2, h), c.o16, (int)(e * 2), 0, 0);
 }
 
-// The epilogue kind of the cheap form (-1: the general epilogue); the
-// output's byte offsets then also fit the buffer resources' 31 bits.
+// The epilogue kind of the cheap form (-1: the general epilogue): its
+// 16-byte (8-byte fp16) stores need a 16-byte aligned output, and the
+// output's byte offsets must fit the buffer resources' 31 bits.
 static int conv_cheap_kind(const ConvParams& p)
 {
     const int k = p.epilogue;
     const bool fits = (size_t)p.batch * p.co * p.ho * p.wo * 4 < (1ull << 30);
-    return !p.residual && fits && (k == 0 || k == 4) ? k : -1;
+    return !p.residual && fits && (uintptr_t)p.out % 16 == 0 && (k == 0 || k == 4) ? k : -1;
 }
 
 template <int NF, int NB, int EK>

@@ -233,6 +233,30 @@ def test_attention_kv_cache_block_mask(gpu, d, tq, count, size, ring, blocks, sp
     np.testing.assert_array_equal(dkc.numpy(), wkc)
 
 
+def test_attention_kv_cache_ring_longer_call(gpu):
+    """A ring call with more new tokens than rows: each row ends up holding the
+    newest position that maps to it (the call's last `size` tokens; no race
+    between the tokens that share a row), and a query whose window lies in
+    the live ring reads them."""
+    rng = np.random.default_rng(41)
+    d, hq, hkv, tq, count, size, span = 64, 2, 1, 100, 10, 64, 32
+    kc, vc = _cache_planes(rng, hkv, size, d, count, True, np.float16)
+    q = draw((1, hq, tq, d), rng, np.float16)
+    k = draw((1, hkv, tq, d), rng, np.float16)
+    v = draw((1, hkv, tq, d), rng, np.float16)
+    D = gpu.DeviceArray.from_numpy
+    dkc, dvc = D(kc), D(vc)
+    out = gpu.DeviceArray((1, tq, hq, d), np.float32)
+    got = gpu.attention(out, D(q), D(k), D(v), causal=True, span=span,
+                        cache=(dkc, dvc, D(np.array([count], np.uint32)), True)).numpy()
+    want, wkc, wvc = oracle.attention_cached(q[0], k, v, kc, vc, count, ring=True, causal=True, span=span)
+    np.testing.assert_array_equal(dkc.numpy(), wkc)
+    np.testing.assert_array_equal(dvc.numpy(), wvc)
+    # queries from position count + tq - size + span - 1 on see only live rows
+    t0 = tq - size + span - 1
+    assert_close(got[0, t0:], want[t0:], FP16)
+
+
 def test_attention_kv_cache_decode_steps(gpu):
     """Decode as a model runs it: one token per call, the count advanced on
     the device between calls; each step matches the reference's formulas over

@@ -841,6 +841,9 @@ __global__ __launch_bounds__(256) void attention_append_kernel(AttnParams p)
     for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
         const uint32_t tok = (uint32_t)(e / HD), d = (uint32_t)(e % HD), pos = cached + tok;
         if (!p.ring && pos >= p.kv_rows) continue;
+        // a ring keeps the call's last kv_rows tokens: an earlier token that a
+        // later one of the same call lands on is not written (no write race)
+        if (p.ring && tok + p.kv_rows < p.tkv) continue;
         const size_t row = p.ring ? pos % p.kv_rows : pos;
         const size_t src = ((size_t)hk * p.tkv + tok) * HD + d, dst = ((size_t)hk * p.kv_rows + row) * HD + d;
         st((void*)p.k, p.kv_dtype, dst, ld(p.k_new, p.new_dtype, src));

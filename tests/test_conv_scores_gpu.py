@@ -291,6 +291,29 @@ def test_conv_cheap_epilogue_unaligned_output(gpu, ks, odt):
     assert_close(out.numpy().astype(np.float32), oracle.conv2d(x, w, b, epi="SILU"), FP16)
 
 
+@pytest.mark.parametrize("ci, co, hi, wi, epi, odt", [
+    (16, 32, 6, 16, "SILU", np.float16),     # one column fragment, one channel block
+    (48, 64, 5, 32, "NONE", np.float32),     # two fragments, two blocks (the second partial)
+    (96, 16, 4, 64, "SILU", np.float32),     # four fragments, three blocks, 16 output channels
+    (128, 80, 3, 80, "NONE", np.float16),    # config 5's row width, four blocks, a channel tail
+    (72, 48, 4, 96, "SILU", np.float16),     # six fragments
+    (40, 64, 3, 112, "SILU", np.float32),    # seven fragments
+    (128, 128, 2, 128, "NONE", np.float32),  # eight fragments (the widest row)
+])
+def test_conv3_cheap_epilogue_widths(gpu, ci, co, hi, wi, epi, odt):
+    """The 3x3 kernel's cheap epilogue at every row width it is compiled for
+    (one to eight 16-column fragments) and one to four channel blocks, both
+    output dtypes: the fragments are stored during the last block, the last
+    after it."""
+    rng = np.random.default_rng(ci * 7 + wi)
+    w = draw(normal((co, ci, 3, 3), 1.0 / np.sqrt(ci * 9)), rng, np.float16)
+    b = draw(normal((co,), 0.1), rng, np.float16)
+    x = draw((1, ci, hi, wi), rng, np.float16)
+    print(f"conv3 cheap widths ci={ci} co={co} hi={hi} wi={wi} {epi} {np.dtype(odt).name}", flush=True)
+    got = run_conv(gpu, x, w, b, out_dtype=odt, epi=epi).astype(np.float32)
+    assert_close(got, oracle.conv2d(x, w, b, epi=epi), FP16)
+
+
 def run_scores(capi, q, k, **kw):
     dq, dk = capi.DeviceArray.from_numpy(q), capi.DeviceArray.from_numpy(k)
     out = capi.DeviceArray(q.shape[:-1] + (k.shape[-2],), np.float32)

@@ -139,8 +139,12 @@ __device__ __forceinline__ float chunk_dot(const WV& w, const XV& x, float s)
 // compiler interleaves each chunk's W and X loads and starts each chunk's
 // products as it lands (config 2 at M = 1: 6.4 us against 6.8 us with the
 // guarded block merged in).
+// W, X, K, N and M also come as leading scalar arguments, which the launch
+// preloads into SGPRs (this file is built with kernarg preloading): the
+// first loads need nothing from the argument struct.
 template <int MP, int R, int KCH, typename TI, typename TW, bool ALL_FULL>
-__global__ __launch_bounds__(256) void slab_reg_kernel(SlabParams a)
+__global__ __launch_bounds__(256) void slab_reg_kernel(const TW* __restrict__ Wp, const TI* __restrict__ Xp, uint32_t Kp,
+                                                       uint32_t Np, uint32_t Mp, SlabParams a)
 {
     typedef typename Vec16<TW>::type wvec;
     constexpr int EPC = Vec16<TW>::n;      // W elements per 16-byte chunk
@@ -152,9 +156,9 @@ __global__ __launch_bounds__(256) void slab_reg_kernel(SlabParams a)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n0 = (blockIdx.x * 4u + wave) * R;
-    const uint32_t K = a.K, N = a.N, M = a.M;
-    const TW* __restrict__ W = (const TW*)a.weight;
-    const TI* __restrict__ X = (const TI*)a.in;
+    const uint32_t K = Kp, N = Np, M = Mp;
+    const TW* __restrict__ W = Wp;
+    const TI* __restrict__ X = Xp;
 
     float acc[V];
 #pragma unroll
@@ -392,9 +396,11 @@ static hipError_t launch_vec(const SlabParams& a, hipStream_t s)
     constexpr uint32_t KB = 64 * KCH * Vec16<TW>::n;
     if constexpr (MP <= 2 || (MP <= 4 && sizeof(TI) == 2)) {
         if (a.N % (4 * R) == 0 && a.K % KB == 0)
-            hipLaunchKernelGGL((slab_reg_kernel<MP, R, KCH, TI, TW, true>), dim3(blocks), dim3(256), 0, s, a);
+            hipLaunchKernelGGL((slab_reg_kernel<MP, R, KCH, TI, TW, true>), dim3(blocks), dim3(256), 0, s,
+                               (const TW*)a.weight, (const TI*)a.in, a.K, a.N, a.M, a);
         else
-            hipLaunchKernelGGL((slab_reg_kernel<MP, R, KCH, TI, TW, false>), dim3(blocks), dim3(256), 0, s, a);
+            hipLaunchKernelGGL((slab_reg_kernel<MP, R, KCH, TI, TW, false>), dim3(blocks), dim3(256), 0, s,
+                               (const TW*)a.weight, (const TI*)a.in, a.K, a.N, a.M, a);
     } else
         hipLaunchKernelGGL((slab_vec_kernel<MP, R, KCH, TI, TW>), dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();

@@ -23,8 +23,10 @@ COMMON = ["-O3", "-fPIC", "-std=c++20", f"--offload-arch={ARCH}", "-I", os.path.
 # The streaming GEMV takes the pointers and sizes its first loads need as
 # leading scalar arguments, which gfx950 can preload into SGPRs at launch (a
 # struct argument is not preloaded): about 0.06 us of a 6.5 us step at M = 1.
-# (The packed MFMA GEMV measured no difference.)
-FILE_FLAGS = {"slab.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
+# (The packed MFMA GEMV measured no difference.) The 3x3 and pointwise conv
+# kernels do the same with their pointers and sizes: about 0.02-0.03 us.
+FILE_FLAGS = {"slab.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+              "conv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 PYMOD_SRC = os.path.join(ENGINE, "pyvai.cpp")

@@ -792,8 +792,14 @@ static int conv_cheap_kind(const ConvParams& p)
 }
 
 template <int NF, int NB, int EK>
-__global__ __launch_bounds__(256) void conv3_pipe_kernel(ConvParams p)
+__global__ __launch_bounds__(256) void conv3_pipe_kernel(const half_t* wp, const void* x, const void* bias_p,
+                                                         const void* scale_p, uint32_t co_n, uint32_t ci_n,
+                                                         uint32_t hi_n, ConvParams pk)
 {
+    // what the entry's loads need, as leading scalar arguments (preloaded
+    // into SGPRs at launch); the rest of the parameters from the struct
+    ConvParams p = pk;
+    p.wp = wp; p.x = x; p.bias = bias_p; p.scale = scale_p; p.co = co_n; p.ci = ci_n; p.hi = hi_n;
     using G = cvp::Geo<NF>;
     using cvp::DPF;
     constexpr uint32_t ROWB = G::ROWB, CHB = G::CHB, CPW = G::CPW, CBB = G::CBB;
@@ -936,7 +942,8 @@ static hipError_t launch_pipe_form(const ConvParams& p, hipStream_t s)
     static PerDevice lds_once;
     hipError_t e = set_max_lds(lds_once, (const void*)conv3_pipe_kernel<NF, NB, EK>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((conv3_pipe_kernel<NF, NB, EK>), dim3((p.co + 63) / 64, p.ho, p.batch), dim3(256), lds, s, p);
+    hipLaunchKernelGGL((conv3_pipe_kernel<NF, NB, EK>), dim3((p.co + 63) / 64, p.ho, p.batch), dim3(256), lds, s,
+                       p.wp, p.x, p.bias, p.scale, p.co, p.ci, p.hi, p);
     return hipGetLastError();
 }
 
@@ -1005,14 +1012,20 @@ __device__ __forceinline__ void conv1_store(const ConvParams& p, const float4v& 
 // MFMA then takes the input as A and the weight as B, so that a lane holds
 // one output channel at four consecutive positions: one 16-byte store.
 template <int NB, int EK>
-__global__ __launch_bounds__(256) void conv1_pipe_kernel(ConvParams p)
+__global__ __launch_bounds__(256) void conv1_pipe_kernel(const half_t* wp, const void* x, const void* bias_p,
+                                                         const void* scale_p, uint32_t co_n, uint32_t ci_n,
+                                                         uint32_t hw_n, ConvParams pk)
 {
+    // what the entry's loads need, as leading scalar arguments (preloaded
+    // into SGPRs at launch); the rest of the parameters from the struct
+    ConvParams p = pk;
+    p.wp = wp; p.x = x; p.bias = bias_p; p.scale = scale_p; p.co = co_n; p.ci = ci_n;
     extern __shared__ half8 smem[];
     __attribute__((address_space(3))) char* xs = (__attribute__((address_space(3))) char*)(
         __attribute__((address_space(3))) void*)smem;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t p0 = blockIdx.x * 16, co0 = blockIdx.y * 64, b = blockIdx.z;
-    const uint32_t HW = p.ho * p.wo;
+    const uint32_t HW = hw_n;
     const int fr = lane & 15, fg = lane >> 4;
     const uint32_t CO16 = (p.co + 15) / 16, oblk = min(blockIdx.y * 4 + wave, CO16 - 1);   // past Co: discarded
 
@@ -1103,7 +1116,7 @@ static hipError_t launch_conv1_form(const ConvParams& p, hipStream_t s)
 {
     const uint32_t HW = p.ho * p.wo;
     hipLaunchKernelGGL((conv1_pipe_kernel<NB, EK>), dim3((HW + 15) / 16, (p.co + 63) / 64, p.batch), dim3(256),
-                       NB * 1024, s, p);
+                       NB * 1024, s, p.wp, p.x, p.bias, p.scale, p.co, p.ci, HW, p);
     return hipGetLastError();
 }
 

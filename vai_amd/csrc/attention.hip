@@ -271,12 +271,6 @@ __global__ __launch_bounds__(256, 1) void attention_fwd_kernel(AttnParams p)
         unit = e1 & 0x3FF;
         h = (e1 >> 10) & 0x3FF;
         b = e1 >> 20;
-        if (chunk == 0 && threadIdx.x == 0) {
-            // the merge pass's index: this query tile's first unit and chunk count
-            uint32_t* tab = p.ws_tab + (((size_t)b * p.hq + h) * nqt + qt) * 2;
-            tab[0] = unit;
-            tab[1] = e0 >> 24;
-        }
     } else {
         // Workgroup -> (query tile, head, batch) with one head's query
         // tiles on one XCD (fa_xcd_block), the longest causal walks first.
@@ -659,10 +653,9 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(AttnParams p)
     constexpr int MAXC = 64, RG = 8;   // chunks per query tile; rows per workgroup
     static_assert(RG * 32 == 256, "one 32-lane group per row");
     __shared__ float wgt[RG][MAXC];
-    const uint32_t nqt = (p.tq + BQ - 1) / BQ, qt = blockIdx.x / (BQ / RG), r0 = (blockIdx.x % (BQ / RG)) * RG;
+    const uint32_t qt = blockIdx.x / (BQ / RG), r0 = (blockIdx.x % (BQ / RG)) * RG;
     const uint32_t h = blockIdx.y, b = blockIdx.z;
-    const uint2 tab = *(const uint2*)(p.ws_tab + (((size_t)b * p.hq + h) * nqt + qt) * 2);
-    const uint32_t u0 = __builtin_amdgcn_readfirstlane(tab.x), nc = __builtin_amdgcn_readfirstlane(tab.y);
+    const uint32_t tab = p.qt_tab[qt], u0 = tab & 0xFFFF, nc = tab >> 16;   // a scalar load of the arguments
     const size_t g0 = ((size_t)b * p.hq + h) * p.units + u0;
     const bool part16 = p.o_dtype == DT_F16;
     // per-row chunk weights 2^(m_c - M) (l_c) / sum_c 2^(m_c - M) l_c: thread t
@@ -895,12 +888,15 @@ void attention_plan(AttnParams& p, uint32_t cus)
             // the units of a head, from the last query tile (the longest
             // causal walks start first), chunk by chunk
             uint32_t uq[AttnParams::FA_WG_TAB], uc[AttnParams::FA_WG_TAB], un[AttnParams::FA_WG_TAB], n = 0;
-            for (uint32_t qt = nqt; qt-- > 0;)
-                for (uint32_t ch = 0, nc = fa_chunks(p, qt, plan_cached(p)); ch < nc; ++ch, ++n) {
+            for (uint32_t qt = nqt; qt-- > 0;) {
+                const uint32_t nc = fa_chunks(p, qt, plan_cached(p));
+                p.qt_tab[qt] = n | nc << 16;
+                for (uint32_t ch = 0; ch < nc; ++ch, ++n) {
                     uq[n] = qt;
                     uc[n] = ch;
                     un[n] = nc;
                 }
+            }
             // workgroup w -> unit of head and batch, a head's units on one XCD
             for (uint32_t w = 0; w < wgs; ++w) {
                 const uint32_t lb = fa_xcd_block(w, (uint32_t)wgs), unit = lb % u, h = (lb / u) % p.hq,
@@ -922,11 +918,8 @@ static size_t attention_kv_bytes(const AttnParams& p)
 
 size_t attention_workspace_bytes(const AttnParams& p)
 {
-    const size_t nqt = (p.tq + fa::BQ - 1) / fa::BQ;
     size_t bytes = attention_kv_bytes(p);
-    if (p.units)
-        bytes += (size_t)p.batch * p.hq * p.units * fa::BQ * (p.dp + 2) * sizeof(float) +
-                 (size_t)p.batch * p.hq * nqt * 2 * sizeof(uint32_t);
+    if (p.units) bytes += (size_t)p.batch * p.hq * p.units * fa::BQ * (p.dp + 2) * sizeof(float);
     return bytes;
 }
 
@@ -936,7 +929,6 @@ void attention_set_workspace(AttnParams& p, void* ws)
     p.ws_kv = kvb ? ws : nullptr;
     p.ws_o = (float*)((char*)ws + kvb);
     p.ws_ml = p.ws_o + (size_t)p.batch * p.hq * p.units * fa::BQ * p.dp;
-    p.ws_tab = (uint32_t*)(p.ws_ml + (size_t)p.batch * p.hq * p.units * fa::BQ * 2);
 }
 
 bool attention_ok(const AttnParams& p)

@@ -184,11 +184,10 @@ struct AttnParams {
     // writes O). Otherwise each query tile's keys are cut into chunks of
     // chunk_tiles 64-key tiles, `units` work units per head; partial O and
     // (max, sum) go to ws_o / ws_ml and a merge pass combines them, finding
-    // each query tile's first unit and chunk count in ws_tab.
+    // each query tile's first unit and chunk count in qt_tab.
     uint32_t units, chunk_tiles;
     float* ws_o;                  // [batch*hq*units][128][dp] (fp32, or fp16 O / l for fp16 output)
     float* ws_ml;                 // [batch*hq*units][128][2]
-    uint32_t* ws_tab;             // [batch*hq*query tiles][2]: first unit, chunks
     void* ws_kv;                  // fp16 copies of fp32 K then V (flash path), else null
     // Split launches run a 1-D grid of units * hq * batch <= FA_WG_TAB
     // workgroups (one round on the GPU, a head's units on one XCD), and
@@ -198,6 +197,10 @@ struct AttnParams {
     // other argument loads, then no divisions.
     static constexpr uint32_t FA_WG_TAB = 256;
     uint32_t wg_tab[2 * FA_WG_TAB];
+    // the merge pass's index, the same for every head: query tile qt's first
+    // unit | its chunk count << 16 (a head has at most FA_WG_TAB units, so at
+    // most that many query tiles)
+    uint32_t qt_tab[FA_WG_TAB];
 };
 bool attention_ok(const AttnParams& p);
 // Units per head for p's shape (0 when no query tile needs splitting), and
